@@ -1,0 +1,168 @@
+/*
+ * lumen_sampler -- MI355X (gfx950) token-sampling engine, C ABI.
+ *
+ * Drop-in for the sampler of Lumen's lumen-runtime
+ * (crates/lumen-runtime/src/sampling.rs). Same parameter surface, same
+ * pipeline order, same results:
+ *   penalties -> top-k -> top-p (T = 1) -> min-p -> temperature -> softmax
+ *   -> inverse-CDF draw; temperature <= 0 is (penalized) greedy argmax.
+ *
+ * Conventions
+ *   - Every call returns 0 (LUMEN_OK) or a negative lumen_status; nothing
+ *     aborts the process.
+ *   - Logits are read from device memory and never modified (stricter than
+ *     the reference, which mutates its slice: sampling.rs:426-428).
+ *   - Host arrays (params, histories, uniforms) are staged by the library;
+ *     the caller may reuse them as soon as the call returns.
+ *   - One lumen_sampler per stream/thread. Calls on one context are
+ *     serialized on the stream they are issued on.
+ *   - A token value of LUMEN_TOKEN_ERROR (0xFFFFFFFF) in the output marks a
+ *     row the engine could not resolve (its trace status says why).
+ */
+#ifndef LUMEN_SAMPLER_H
+#define LUMEN_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lumen_sampler lumen_sampler;
+typedef struct ihipStream_t *lumen_stream;  /* hipStream_t */
+
+typedef enum {
+    LUMEN_OK = 0,
+    LUMEN_ERR_INVALID = -1,      /* bad argument (null pointer, shape, dtype) */
+    LUMEN_ERR_HIP = -2,          /* a HIP runtime call failed */
+    LUMEN_ERR_CODE_OBJECT = -3,  /* the gfx950 code object is missing/corrupt */
+    LUMEN_ERR_NO_DEVICE = -4,
+    LUMEN_ERR_UNSUPPORTED = -5,  /* a row needs a feature this build lacks */
+    LUMEN_ERR_ROW = -6,          /* at least one row reported a failure */
+} lumen_status;
+
+#define LUMEN_TOKEN_ERROR 0xFFFFFFFFu
+
+typedef enum { LUMEN_DTYPE_F32 = 0, LUMEN_DTYPE_BF16 = 1 } lumen_dtype;
+
+/*
+ * Sampling parameters, one per row. Mirrors SamplingParams
+ * (sampling.rs:239-325). Each `Option<_>` field is encoded by the value the
+ * reference treats exactly like `None`:
+ *   top_k 0, top_p 1.0, min_p 0.0, repetition_penalty 1.0,
+ *   presence_penalty 0.0, frequency_penalty 0.0, repeat_last_n 0.
+ * `seed` is not part of a per-call row: callers hold the RNG
+ * (lumen_xorshift64_*) or pass uniforms directly.
+ */
+typedef struct {
+    float temperature;          /* <= 0: greedy */
+    float top_p;
+    float min_p;
+    float repetition_penalty;
+    float presence_penalty;
+    float frequency_penalty;
+    uint64_t top_k;
+    uint64_t repeat_last_n;
+    int32_t anti_restate;       /* greedy anti-degeneration guard; not supported on
+                                   the GPU path yet: rows that set it are rejected
+                                   with LUMEN_ERR_UNSUPPORTED */
+    int32_t reserved;
+} lumen_sampling_params;
+
+/* Per-row diagnostics (optional). */
+typedef struct {
+    uint32_t status;           /* 0 ok; 1 tie overflow; 2 internal list overflow */
+    uint32_t path;             /* bit0 greedy, bit1 LDS path, bit2 streaming path,
+                                  bit3 uniform top-p, bit4 uniform final, bit5 NaN */
+    uint32_t topk_cutoff_key;  /* f32::total_cmp key of the k-th largest logit */
+    uint32_t topk_survivors;
+    float topp_sum;            /* softmax sum inside top-p */
+    uint32_t topp_kept;        /* `kept` of sampling.rs:956-963 (V if never broke) */
+    float topp_cum;
+    uint32_t windows;
+    float final_max;
+    float final_sum;
+    float cdf_before;
+    float cdf_at;
+    uint32_t token;
+    uint32_t passes;           /* streaming passes over the row */
+    uint32_t pad[2];
+} lumen_row_trace;
+
+/*
+ * One batch. Row b of the logits starts at logits + b * row_stride
+ * elements. Histories are the SamplerState::history of each row
+ * (sampling.rs:352-393), flattened: row b uses
+ * history[history_offsets[b] .. history_offsets[b+1]). The library applies
+ * the repeat_last_n window and counts occurrences exactly as
+ * apply_penalties (sampling.rs:850-879). history_offsets may be NULL (no
+ * history for any row).
+ *
+ * The draw of row b is uniforms[b] in [0, 1). When rng_states is non-NULL
+ * the library instead draws Xorshift64::next_f32 from rng_states[b]
+ * (advancing it in place) for every row with temperature > 0, matching
+ * `sample_logits(.., rng)` (sampling.rs:1004). Greedy rows consume no draw.
+ */
+typedef struct {
+    const void *logits;                 /* device */
+    int32_t dtype;                      /* lumen_dtype */
+    uint32_t batch;
+    uint32_t vocab;
+    uint64_t row_stride;                /* elements between row starts */
+    const lumen_sampling_params *params;/* host, [batch] */
+    /* Penalty window, form A (host): raw SamplerState::history per row; the
+     * library applies repeat_last_n and counts occurrences. */
+    const uint64_t *history_offsets;    /* host, [batch + 1] or NULL */
+    const uint32_t *history;            /* host */
+    /* Penalty window, form B (device, pre-counted): the distinct token ids of
+     * each row's window and their counts -- the SamplerState::freq map
+     * (sampling.rs:356) kept resident by the caller. Row b uses entries
+     * [pen_offsets[b], pen_offsets[b+1]). Used instead of form A when
+     * pen_offsets is non-NULL; the caller has already applied the window. */
+    const uint32_t *pen_offsets;        /* device, [batch + 1] or NULL */
+    const uint32_t *pen_ids;            /* device */
+    const uint32_t *pen_counts;         /* device */
+    const float *uniforms;              /* host, [batch]; may be NULL if rng_states */
+    uint64_t *rng_states;               /* host, [batch] in/out; may be NULL */
+    uint32_t *tokens;                   /* device, [batch] output */
+    lumen_row_trace *trace;             /* device, [batch] or NULL */
+    float *penalized_out;               /* device, [batch][vocab] or NULL (debug) */
+} lumen_batch;
+
+/* Context: loads the gfx950 code object on `device`. The code object is
+ * embedded in the library; LUMEN_SAMPLER_CODE_OBJECT=<path> overrides it. */
+int lumen_sampler_create(lumen_sampler **out, int device);
+void lumen_sampler_destroy(lumen_sampler *s);
+
+/* Batched sampler. Asynchronous on `stream` (host inputs are staged before
+ * return). Replaces sample_logits (sampling.rs:452-527) applied to every
+ * row, and the GPU hook ComputeBackend::decode_token_sampled
+ * (compute/mod.rs:424-438). */
+int lumen_sampler_sample_batch(lumen_sampler *s, const lumen_batch *batch, lumen_stream stream);
+
+/* Synchronous convenience: same as above, then waits and copies the tokens
+ * to host memory. Returns LUMEN_ERR_ROW if a row reported a failure.
+ * Mirrors Sampler::sample / sample_token_with_state (sampling.rs:429-433,
+ * engine.rs:80-88) for a batch. */
+int lumen_sampler_sample_batch_sync(lumen_sampler *s, const lumen_batch *batch,
+                                    uint32_t *tokens_host, lumen_stream stream);
+
+/* Reference RNG (sampling.rs:45-106): Xorshift64 seeded through the
+ * SplitMix64 finalizer. */
+uint64_t lumen_xorshift64_new(uint64_t seed);
+uint64_t lumen_xorshift64_next_u64(uint64_t *state);
+float lumen_xorshift64_next_f32(uint64_t *state);
+
+/* Library / code-object version string. */
+const char *lumen_sampler_version(void);
+
+/* Human-readable reason for the last failing call on this thread. The
+ * reference's backend hooks return RuntimeError strings
+ * (compute/mod.rs:424-438); this is their C-ABI counterpart. */
+const char *lumen_sampler_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LUMEN_SAMPLER_H */

@@ -1,0 +1,85 @@
+// Structures shared by the host library (sampler_host.cpp) and the gfx950
+// code object (sampler_kernels.hip). Plain C layout, no HIP types.
+#pragma once
+#include <stdint.h>
+
+namespace lumen {
+
+// Per-row parameters resolved on the host exactly as the reference decides
+// which stages run (crates/lumen-runtime/src/sampling.rs:452-527).
+struct RowParams {
+  float temperature;  // <= 0 selects greedy (sampling.rs:468)
+  float inv_temp;     // 1.0f / temperature, computed once in f32 (sampling.rs:517)
+  float top_p;        // used iff kTopP
+  float log_min_p;    // logf(min_p) (sampling.rs:989), used iff kMinP
+  float rep;          // repetition penalty
+  float presence;     // presence penalty
+  float freq;         // frequency penalty
+  uint32_t top_k;     // used iff kTopK; 1 <= top_k < V
+  uint32_t flags;
+  uint32_t pad[3];
+};
+
+enum RowFlags : uint32_t {
+  kGreedy = 1u,   // temperature <= 0
+  kPen = 2u,      // penalties_active() and a non-empty window (sampling.rs:332-337, 858)
+  kRep = 4u,      // |rep - 1| >= f32::EPSILON (sampling.rs:887)
+  kTopK = 8u,     // 0 < k < V (sampling.rs:493)
+  kTopP = 16u,    // 0 < p < 1 (sampling.rs:503)
+  kMinP = 32u,    // min_p > 0 (sampling.rs:511)
+};
+
+// Per-row diagnostics (optional output), mirrors the oracle's trace.
+struct RowTrace {
+  uint32_t status;          // 0 ok, else a RowStatus code
+  uint32_t path;            // bit0 greedy, bit1 small path, bit2 large path, bit3 uniform top-p,
+                            // bit4 uniform final, bit5 NaN final
+  uint32_t topk_cutoff_key; // total_cmp key of the k-th largest logit
+  uint32_t topk_survivors;
+  float topp_sum;           // softmax sum inside top-p
+  uint32_t topp_kept;       // reference `kept` (V when the loop never broke)
+  float topp_cum;           // cum value at the crossing
+  uint32_t windows;         // top-p windows walked
+  float final_max;
+  float final_sum;
+  float cdf_before;
+  float cdf_at;
+  uint32_t token;
+  uint32_t passes;          // full-row passes made over the logits
+  uint32_t pad[2];
+};
+
+enum RowStatus : uint32_t {
+  kStatusOk = 0,
+  kStatusTieOverflow = 1,   // > list capacity of exactly-equal keys in one top-p window
+  kStatusListOverflow = 2,  // internal: window larger than planned
+};
+
+constexpr int kInlineRows = 8;
+
+struct KernelArgs {
+  const void* logits;        // [B][row_stride] f32 or bf16, device
+  uint64_t row_stride;       // elements
+  uint32_t vocab;
+  uint32_t batch;
+  int32_t dtype;             // 0 = f32, 1 = bf16
+  uint32_t pad0;
+  const RowParams* params;   // [B] device
+  const uint32_t* hist_off;  // [B+1] offsets into hist_ids / hist_cnt
+  const uint32_t* hist_ids;  // unique token ids of the penalty window, per row
+  const uint32_t* hist_cnt;  // occurrence counts
+  const float* uniforms;     // [B] draw per row (ignored by greedy rows)
+  uint32_t* tokens;          // [B] output
+  RowTrace* trace;           // [B] optional
+  float* pen_scratch;        // [B][pen_stride] penalized rows (f32)
+  uint64_t pen_stride;
+  float* pen_out;            // optional [B][vocab] copy of penalized logits
+  // Small batches pass their parameters and draws inside the kernel
+  // arguments (no staging copy): used when inline_rows > 0.
+  uint32_t inline_rows;
+  uint32_t pad1;
+  float inline_uniforms[kInlineRows];
+  RowParams inline_params[kInlineRows];
+};
+
+}  // namespace lumen

@@ -1,0 +1,420 @@
+// Host side of the gfx950 sampling engine: the C ABI of include/lumen_sampler.h.
+//
+// Responsibilities:
+//  * load the gfx950 code object (embedded with .incbin, or a file named by
+//    LUMEN_SAMPLER_CODE_OBJECT) through hipModuleLoadData;
+//  * resolve each row's SamplingParams into the stage flags exactly as the
+//    reference decides them (crates/lumen-runtime/src/sampling.rs:452-527);
+//  * build the penalty window counts from raw histories (form A,
+//    sampling.rs:850-879) or take caller-resident counts (form B);
+//  * stage small host inputs (inline kernel arguments for up to 8 rows, a
+//    pinned staging buffer otherwise) and launch one workgroup per row.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "../../include/lumen_sampler.h"
+#include "kernel_abi.h"
+
+extern "C" const unsigned char lumen_gfx950_code_object[];
+extern "C" const unsigned char lumen_gfx950_code_object_end[];
+
+using lumen::KernelArgs;
+using lumen::RowParams;
+
+namespace {
+
+constexpr float kF32Eps = 1.1920929e-7f;  // f32::EPSILON
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+
+}  // namespace
+
+struct lumen_sampler {
+  int device = 0;
+  hipModule_t module = nullptr;
+  hipFunction_t fn = nullptr;
+  // staging: one pinned host block and one device block, same layout
+  void* pin = nullptr;
+  size_t pin_cap = 0;
+  DevBuf stage;
+  DevBuf pen_scratch;
+  hipEvent_t staged = nullptr;  // recorded after the last staging copy
+  bool staged_pending = false;
+  std::vector<uint32_t> ids, cnts, offs;
+  std::vector<uint32_t> tmp;
+};
+
+namespace {
+
+thread_local char g_last_error[256] = "";
+
+int fail(int code, const char* why) {
+  std::snprintf(g_last_error, sizeof g_last_error, "%s", why);
+  return code;
+}
+
+int hip_fail(hipError_t e) {
+  if (e == hipSuccess) return LUMEN_OK;
+  std::snprintf(g_last_error, sizeof g_last_error, "HIP error: %s", hipGetErrorString(e));
+  return LUMEN_ERR_HIP;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+int ensure_dev(DevBuf& b, size_t bytes) {
+  if (b.cap >= bytes) return LUMEN_OK;
+  if (b.p) {
+    if (hipDeviceSynchronize() != hipSuccess) return LUMEN_ERR_HIP;
+    (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+  }
+  size_t cap = std::max<size_t>(bytes, 4096);
+  if (hipMalloc(&b.p, cap) != hipSuccess) return LUMEN_ERR_HIP;
+  b.cap = cap;
+  return LUMEN_OK;
+}
+
+// Resolves one row (sampling.rs:452-527). Returns LUMEN_OK or an error.
+int resolve_row(const lumen_sampling_params& p, uint32_t V, bool has_window, RowParams& r) {
+  std::memset(&r, 0, sizeof(r));
+  r.temperature = p.temperature;
+  const float rep = p.repetition_penalty, pres = p.presence_penalty, freq = p.frequency_penalty;
+  // penalties_active (sampling.rs:332-337); apply_penalties returns early on
+  // an empty history (:858)
+  const bool pen = std::fabs(rep - 1.0f) >= kF32Eps || pres != 0.0f || freq != 0.0f;
+  r.rep = rep;
+  r.presence = pres;
+  r.freq = freq;
+  if (pen && has_window) r.flags |= lumen::kPen;
+  if (std::fabs(rep - 1.0f) >= kF32Eps) r.flags |= lumen::kRep;
+  if (p.temperature <= 0.0f) {  // greedy branch (sampling.rs:468)
+    if (p.anti_restate) return LUMEN_ERR_UNSUPPORTED;
+    r.flags |= lumen::kGreedy;
+    return LUMEN_OK;
+  }
+  if (p.top_k > 0 && p.top_k < (uint64_t)V) {  // sampling.rs:492-496
+    r.flags |= lumen::kTopK;
+    r.top_k = (uint32_t)p.top_k;
+  }
+  if (p.top_p > 0.0f && p.top_p < 1.0f) {  // sampling.rs:502-506
+    r.flags |= lumen::kTopP;
+    r.top_p = p.top_p;
+  }
+  if (p.min_p > 0.0f) {  // sampling.rs:510-514; ln() as in :989
+    r.flags |= lumen::kMinP;
+    r.log_min_p = logf(p.min_p);
+  }
+  r.inv_temp = 1.0f / p.temperature;  // sampling.rs:517
+  return LUMEN_OK;
+}
+
+// Form A: counts over the last repeat_last_n ids of the history
+// (sampling.rs:860-878), appended as (id, count) with ascending ids.
+void count_window(lumen_sampler* s, const uint32_t* h, uint64_t len, uint64_t window) {
+  uint64_t start = 0;
+  if (window > 0 && window < len) start = len - window;
+  s->tmp.assign(h + start, h + len);
+  std::sort(s->tmp.begin(), s->tmp.end());
+  for (size_t i = 0; i < s->tmp.size();) {
+    size_t j = i;
+    while (j < s->tmp.size() && s->tmp[j] == s->tmp[i]) ++j;
+    s->ids.push_back(s->tmp[i]);
+    s->cnts.push_back((uint32_t)(j - i));
+    i = j;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t lumen_xorshift64_new(uint64_t seed) {
+  // sampling.rs:64-83
+  uint64_t base = seed == 0 ? 0xDEADBEEFCAFEBABEull : seed;
+  uint64_t x = base + 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  x ^= x >> 31;
+  return x == 0 ? 0xDEADBEEFCAFEBABEull : x;
+}
+
+uint64_t lumen_xorshift64_next_u64(uint64_t* state) {
+  // sampling.rs:86-93
+  uint64_t x = *state;
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  *state = x;
+  return x;
+}
+
+float lumen_xorshift64_next_f32(uint64_t* state) {
+  // sampling.rs:96-99
+  const float scale = 1.0f / (float)(1ull << 24);
+  return (float)(lumen_xorshift64_next_u64(state) >> 40) * scale;
+}
+
+const char* lumen_sampler_version(void) { return "lumen_sampler 0.1.0 gfx950"; }
+
+const char* lumen_sampler_last_error(void) { return g_last_error; }
+
+int lumen_sampler_create(lumen_sampler** out, int device) {
+  if (!out) return LUMEN_ERR_INVALID;
+  *out = nullptr;
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return LUMEN_ERR_NO_DEVICE;
+  if (device < 0 || device >= ndev) return LUMEN_ERR_INVALID;
+  DeviceGuard g(device);
+  lumen_sampler* s = new (std::nothrow) lumen_sampler();
+  if (!s) return LUMEN_ERR_INVALID;
+  s->device = device;
+  std::vector<char> file;
+  const void* image = lumen_gfx950_code_object;
+  if (const char* path = std::getenv("LUMEN_SAMPLER_CODE_OBJECT")) {
+    FILE* f = std::fopen(path, "rb");
+    if (!f) {
+      delete s;
+      return LUMEN_ERR_CODE_OBJECT;
+    }
+    char buf[65536];
+    size_t n;
+    while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) file.insert(file.end(), buf, buf + n);
+    std::fclose(f);
+    if (file.empty()) {
+      delete s;
+      return LUMEN_ERR_CODE_OBJECT;
+    }
+    image = file.data();
+  } else if (lumen_gfx950_code_object_end == lumen_gfx950_code_object) {
+    delete s;
+    return LUMEN_ERR_CODE_OBJECT;
+  }
+  if (hipModuleLoadData(&s->module, image) != hipSuccess) {
+    (void)hipGetLastError();
+    delete s;
+    return LUMEN_ERR_CODE_OBJECT;
+  }
+  if (hipModuleGetFunction(&s->fn, s->module, "lumen_sample_rows") != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipModuleUnload(s->module);
+    delete s;
+    return LUMEN_ERR_CODE_OBJECT;
+  }
+  if (hipEventCreateWithFlags(&s->staged, hipEventDisableTiming) != hipSuccess) {
+    (void)hipModuleUnload(s->module);
+    delete s;
+    return LUMEN_ERR_HIP;
+  }
+  *out = s;
+  return LUMEN_OK;
+}
+
+void lumen_sampler_destroy(lumen_sampler* s) {
+  if (!s) return;
+  DeviceGuard g(s->device);
+  (void)hipDeviceSynchronize();
+  if (s->pin) (void)hipHostFree(s->pin);
+  if (s->stage.p) (void)hipFree(s->stage.p);
+  if (s->pen_scratch.p) (void)hipFree(s->pen_scratch.p);
+  if (s->staged) (void)hipEventDestroy(s->staged);
+  if (s->module) (void)hipModuleUnload(s->module);
+  delete s;
+}
+
+int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream) {
+  if (!s || !bt) return fail(LUMEN_ERR_INVALID, "null context or batch");
+  const uint32_t B = bt->batch, V = bt->vocab;
+  if (B == 0) return LUMEN_OK;
+  if (!bt->params || !bt->tokens) return fail(LUMEN_ERR_INVALID, "params and tokens are required");
+  if (bt->dtype != LUMEN_DTYPE_F32 && bt->dtype != LUMEN_DTYPE_BF16)
+    return fail(LUMEN_ERR_INVALID, "dtype must be LUMEN_DTYPE_F32 or LUMEN_DTYPE_BF16");
+  if (V > 0 && (!bt->logits || bt->row_stride < V))
+    return fail(LUMEN_ERR_INVALID, "logits missing or row_stride < vocab");
+  if (!bt->uniforms && !bt->rng_states) {
+    for (uint32_t b = 0; b < B; ++b)
+      if (bt->params[b].temperature > 0.0f)
+        return fail(LUMEN_ERR_INVALID, "sampled rows need uniforms or rng_states");
+  }
+  if (bt->pen_offsets && (!bt->pen_ids || !bt->pen_counts))
+    return fail(LUMEN_ERR_INVALID, "pen_offsets needs pen_ids and pen_counts");
+  if (bt->history_offsets && !bt->history && bt->history_offsets[B] > 0)
+    return fail(LUMEN_ERR_INVALID, "history_offsets without history");
+  DeviceGuard g(s->device);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+
+  // rows, draws, penalty windows (host side)
+  std::vector<RowParams> rows(B);
+  std::vector<float> draws(B, 0.0f);
+  s->ids.clear();
+  s->cnts.clear();
+  s->offs.assign(B + 1, 0);
+  bool any_pen = false;
+  for (uint32_t b = 0; b < B; ++b) {
+    const lumen_sampling_params& p = bt->params[b];
+    bool has_window = false;
+    uint64_t h0 = 0, h1 = 0;
+    if (!bt->pen_offsets && bt->history_offsets) {
+      h0 = bt->history_offsets[b];
+      h1 = bt->history_offsets[b + 1];
+      if (h1 < h0) return fail(LUMEN_ERR_INVALID, "history_offsets must be non-decreasing");
+      has_window = h1 > h0;
+    } else if (bt->pen_offsets) {
+      has_window = true;  // an empty count range applies nothing either way
+    }
+    int rc = resolve_row(p, V, has_window, rows[b]);
+    if (rc != LUMEN_OK) return fail(rc, "anti_restate is not supported on the GPU path");
+    if (!bt->pen_offsets && (rows[b].flags & lumen::kPen))
+      count_window(s, bt->history + h0, h1 - h0, p.repeat_last_n);
+    s->offs[b + 1] = (uint32_t)s->ids.size();
+    any_pen |= (rows[b].flags & lumen::kPen) != 0;
+    if (V > 0 && !(rows[b].flags & lumen::kGreedy)) {
+      // exactly one draw per sampled row (sampling.rs:1004)
+      draws[b] = bt->rng_states ? lumen_xorshift64_next_f32(&bt->rng_states[b]) : bt->uniforms[b];
+    }
+  }
+  if (V == 0) {
+    // sampling.rs:458-460: empty logits sample token 0 and draw nothing.
+    // Written with a copy (not a memset node) so the call stays capturable.
+    if (s->staged_pending) {
+      if (hipEventSynchronize(s->staged) != hipSuccess) return LUMEN_ERR_HIP;
+      s->staged_pending = false;
+    }
+    const size_t bytes = sizeof(uint32_t) * B;
+    if (s->pin_cap < bytes) {
+      if (s->pin) (void)hipHostFree(s->pin);
+      s->pin = nullptr;
+      s->pin_cap = 0;
+      size_t cap = std::max<size_t>(bytes, 65536);
+      if (hipHostMalloc(&s->pin, cap, hipHostMallocDefault) != hipSuccess) return LUMEN_ERR_HIP;
+      s->pin_cap = cap;
+    }
+    std::memset(s->pin, 0, bytes);
+    if (hipMemcpyAsync(bt->tokens, s->pin, bytes, hipMemcpyHostToDevice, st) != hipSuccess)
+      return LUMEN_ERR_HIP;
+    if (hipEventRecord(s->staged, st) != hipSuccess) return LUMEN_ERR_HIP;
+    s->staged_pending = true;
+    return LUMEN_OK;
+  }
+
+  KernelArgs ka;
+  std::memset(&ka, 0, sizeof(ka));
+  ka.logits = bt->logits;
+  ka.row_stride = bt->row_stride;
+  ka.vocab = V;
+  ka.batch = B;
+  ka.dtype = bt->dtype;
+  ka.tokens = bt->tokens;
+  ka.trace = reinterpret_cast<lumen::RowTrace*>(bt->trace);
+  ka.pen_out = bt->penalized_out;
+
+  // staging layout: [params][uniforms][offs][ids][cnts]
+  const bool inl = B <= (uint32_t)lumen::kInlineRows;
+  const bool host_csr = !bt->pen_offsets;
+  size_t off_params = 0;
+  size_t off_unif = off_params + (inl ? 0 : sizeof(RowParams) * B);
+  size_t off_offs = (off_unif + (inl ? 0 : sizeof(float) * B) + 15) & ~size_t(15);
+  size_t off_ids = off_offs + (host_csr ? sizeof(uint32_t) * (B + 1) : 0);
+  size_t off_cnts = off_ids + (host_csr ? sizeof(uint32_t) * s->ids.size() : 0);
+  size_t total = off_cnts + (host_csr ? sizeof(uint32_t) * s->cnts.size() : 0);
+  if (inl) {
+    ka.inline_rows = B;
+    for (uint32_t b = 0; b < B; ++b) {
+      ka.inline_params[b] = rows[b];
+      ka.inline_uniforms[b] = draws[b];
+    }
+  }
+  if (total > 0) {
+    if (s->staged_pending) {
+      if (hipEventSynchronize(s->staged) != hipSuccess) return LUMEN_ERR_HIP;
+      s->staged_pending = false;
+    }
+    if (s->pin_cap < total) {
+      if (s->pin) (void)hipHostFree(s->pin);
+      s->pin = nullptr;
+      s->pin_cap = 0;
+      size_t cap = std::max<size_t>(total, 65536);
+      if (hipHostMalloc(&s->pin, cap, hipHostMallocDefault) != hipSuccess) return LUMEN_ERR_HIP;
+      s->pin_cap = cap;
+    }
+    int rc = ensure_dev(s->stage, total);
+    if (rc != LUMEN_OK) return rc;
+    char* hp = static_cast<char*>(s->pin);
+    char* dp = static_cast<char*>(s->stage.p);
+    if (!inl) {
+      std::memcpy(hp + off_params, rows.data(), sizeof(RowParams) * B);
+      std::memcpy(hp + off_unif, draws.data(), sizeof(float) * B);
+      ka.params = reinterpret_cast<const RowParams*>(dp + off_params);
+      ka.uniforms = reinterpret_cast<const float*>(dp + off_unif);
+    }
+    if (host_csr) {
+      std::memcpy(hp + off_offs, s->offs.data(), sizeof(uint32_t) * (B + 1));
+      if (!s->ids.empty()) {
+        std::memcpy(hp + off_ids, s->ids.data(), sizeof(uint32_t) * s->ids.size());
+        std::memcpy(hp + off_cnts, s->cnts.data(), sizeof(uint32_t) * s->cnts.size());
+      }
+      ka.hist_off = reinterpret_cast<const uint32_t*>(dp + off_offs);
+      ka.hist_ids = reinterpret_cast<const uint32_t*>(dp + off_ids);
+      ka.hist_cnt = reinterpret_cast<const uint32_t*>(dp + off_cnts);
+    }
+    if (hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, st) != hipSuccess) return LUMEN_ERR_HIP;
+    if (hipEventRecord(s->staged, st) != hipSuccess) return LUMEN_ERR_HIP;
+    s->staged_pending = true;
+  }
+  if (!host_csr) {
+    ka.hist_off = bt->pen_offsets;
+    ka.hist_ids = bt->pen_ids;
+    ka.hist_cnt = bt->pen_counts;
+  }
+  if (any_pen) {
+    const uint64_t stride = ((uint64_t)V + 63) & ~uint64_t(63);
+    int rc = ensure_dev(s->pen_scratch, sizeof(float) * stride * B);
+    if (rc != LUMEN_OK) return rc;
+    ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
+    ka.pen_stride = stride;
+  }
+  size_t argsz = sizeof(ka);
+  void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &argsz,
+                 HIP_LAUNCH_PARAM_END};
+  hipError_t e = hipModuleLaunchKernel(s->fn, B, 1, 1, 1024, 1, 1, 0, st, nullptr, cfg);
+  return hip_fail(e);
+}
+
+int lumen_sampler_sample_batch_sync(lumen_sampler* s, const lumen_batch* bt, uint32_t* tokens_host,
+                                    lumen_stream stream) {
+  if (!tokens_host) return fail(LUMEN_ERR_INVALID, "tokens_host is required");
+  int rc = lumen_sampler_sample_batch(s, bt, stream);
+  if (rc != LUMEN_OK) return rc;
+  DeviceGuard g(s->device);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(tokens_host, bt->tokens, sizeof(uint32_t) * bt->batch, hipMemcpyDeviceToHost,
+                     st) != hipSuccess)
+    return LUMEN_ERR_HIP;
+  if (hipStreamSynchronize(st) != hipSuccess) return LUMEN_ERR_HIP;
+  for (uint32_t b = 0; b < bt->batch; ++b)
+    if (tokens_host[b] == LUMEN_TOKEN_ERROR) return fail(LUMEN_ERR_ROW, "a row reported a failure (see its trace status)");
+  return LUMEN_OK;
+}
+
+}  // extern "C"

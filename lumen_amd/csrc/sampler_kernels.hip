@@ -1,0 +1,949 @@
+// gfx950 token-sampling engine: one workgroup (1024 threads, 16 wave64s)
+// per [V]-row of logits, all stages of Lumen's CPU sampler in one launch.
+//
+// Reference semantics: crates/lumen-runtime/src/sampling.rs:452-527
+//   penalties (:850-900) -> top-k (:904-933) -> top-p on T=1 logits
+//   (:942-967) -> min-p (:976-994) -> temperature (:516-520) -> softmax
+//   (:207-231) -> inverse-CDF draw (:1003-1014); greedy rows take
+//   penalties -> argmax (:468-476, :538-547).
+//
+// Exactness: every f32 operation of the reference is performed as the same
+// single IEEE operation (this file is compiled with -ffp-contract=off and
+// uses explicit _rn intrinsics on the penalty/temperature/division paths);
+// expf is the glibc restatement in expf_glibc.h; every sequential f32 sum of
+// the reference is reproduced bit-exactly by ecss.h. Orderings use the
+// total_cmp key (sign-flipped bits) with lowest-index tie breaks.
+//
+// Data flow per row:
+//   * penalized rows are first materialized into a scratch row (the input
+//     logits are never modified);
+//   * top-k: radix descent on 11/11/10-bit digits of the key with LDS
+//     histograms; once the candidates above the current digit fit the LDS
+//     list (8192 entries) they are compacted and the cutoff is finished with
+//     an LDS bitonic sort. All ties at the cutoff survive (k == 1 keeps the
+//     lowest-index maximum);
+//   * small path: everything after top-k runs on the LDS list (index order),
+//     with LDS sorts for the top-p order;
+//   * large path (no top-k, or too many survivors): streaming passes over the
+//     row; top-p walks the probability order in windows of at most 8192
+//     candidates, each window compacted into LDS and sorted, carrying the
+//     exact cumulative sum across windows.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ecss.h"
+#include "expf_glibc.h"
+#include "kernel_abi.h"
+
+namespace lumen {
+
+constexpr int kCap = 8192;          // LDS list capacity (entries)
+constexpr int kCapWindow = kCap - 512;  // planned window size (margin for equal-probability spill)
+constexpr float kNegInf = -__builtin_huge_valf();
+
+struct Smem {
+  uint64_t A[kCap];
+  uint64_t Bk[kCap];
+  uint32_t H[2048];
+  uint32_t H0[2048];
+  EcssShared ecss;
+  uint32_t red_a[kWaves];
+  uint32_t red_b[kWaves];
+  float red_f[kWaves];
+  uint32_t cnt;
+  int misc_i[4];
+  uint32_t misc_u[4];
+};
+
+// ---------------------------------------------------------------- helpers
+
+__device__ __forceinline__ uint32_t tkey(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key2f(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+__device__ __forceinline__ bool is_nan(float f) { return (__float_as_uint(f) & 0x7fffffffu) > 0x7f800000u; }
+__device__ __forceinline__ bool is_finite(float f) { return (__float_as_uint(f) & 0x7f800000u) != 0x7f800000u; }
+// f32::max: a NaN operand yields the other operand.
+__device__ __forceinline__ float rmax(float a, float b) {
+  if (is_nan(b)) return a;
+  if (is_nan(a)) return b;
+  return a > b ? a : b;
+}
+
+struct Row {
+  const float* f;
+  const uint16_t* h;
+  uint32_t V;
+  bool vec;
+  __device__ __forceinline__ float at(uint32_t i) const {
+    return f ? f[i] : __uint_as_float((uint32_t)h[i] << 16);
+  }
+  // elements i..i+3 (i % 4 == 0); out-of-range lanes are left untouched
+  __device__ __forceinline__ void load4(uint32_t i, float (&v)[4]) const {
+    if (vec && i + 3 < V) {
+      if (f) {
+        float4 q = *reinterpret_cast<const float4*>(f + i);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+      } else {
+        ushort4 q = *reinterpret_cast<const ushort4*>(h + i);
+        v[0] = __uint_as_float((uint32_t)q.x << 16);
+        v[1] = __uint_as_float((uint32_t)q.y << 16);
+        v[2] = __uint_as_float((uint32_t)q.z << 16);
+        v[3] = __uint_as_float((uint32_t)q.w << 16);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i + j < V) v[j] = at(i + j);
+    }
+  }
+};
+
+// f(i, v) for every element of the row; each thread handles 4 groups of 4
+// consecutive elements per iteration to keep several loads in flight.
+template <class F>
+__device__ __forceinline__ void row_foreach(const Row& r, F&& f) {
+  const uint32_t V = r.V;
+  for (uint32_t g0 = threadIdx.x; g0 * 4u < V; g0 += 4u * kThreads) {
+    float v[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t i = (g0 + u * kThreads) * 4u;
+      if (i < V) r.load4(i, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t i = (g0 + u * kThreads) * 4u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i + j < V) f(i + j, v[u][j]);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_sum_u32(v);
+  if (lane == 0) s.red_a[w] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r += s.red_a[i];
+  __syncthreads();
+  return r;
+}
+
+__device__ uint32_t block_or_u32(uint32_t v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+  if (lane == 0) s.red_a[w] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r |= s.red_a[i];
+  __syncthreads();
+  return r;
+}
+
+// max of a 64-bit value carried as (hi, lo)
+__device__ uint64_t block_max_u64(uint64_t v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+    uint32_t lo = __shfl_xor((uint32_t)v, o, 64);
+    uint64_t u = ((uint64_t)hi << 32) | lo;
+    v = u > v ? u : v;
+  }
+  if (lane == 0) {
+    s.red_a[w] = (uint32_t)(v >> 32);
+    s.red_b[w] = (uint32_t)v;
+  }
+  __syncthreads();
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    uint64_t u = ((uint64_t)s.red_a[i] << 32) | s.red_b[i];
+    r = u > r ? u : r;
+  }
+  __syncthreads();
+  return r;
+}
+
+// fold(-inf, f32::max) over the block; NaN inputs are ignored
+__device__ float block_rmax(float v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = rmax(v, __shfl_xor(v, o, 64));
+  if (lane == 0) s.red_f[w] = v;
+  __syncthreads();
+  float r = kNegInf;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r = rmax(r, s.red_f[i]);
+  __syncthreads();
+  return r;
+}
+
+__device__ uint32_t block_incl_scan_u32(uint32_t v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) s.red_a[w] = v;
+  __syncthreads();
+  uint32_t pre = 0;
+  for (int i = 0; i < w; ++i) pre += s.red_a[i];
+  __syncthreads();
+  return v + pre;
+}
+
+// Histogram search from the top digit down: returns d with
+// above(d) < need <= above(d) + H[d], above(d) = sum of H over digits > d.
+// d = -1 when the total is below `need` (then *above = total).
+__device__ int find_from_top(const uint32_t* H, int nb, uint32_t need, uint32_t* above, Smem& s) {
+  const int t = threadIdx.x;
+  const int per = nb / kThreads;  // 1 or 2
+  uint32_t loc = 0;
+  for (int q = 0; q < per; ++q) loc += H[nb - 1 - per * t - q];
+  uint32_t incl = block_incl_scan_u32(loc, s);
+  uint32_t ex = incl - loc;
+  if (t == 0) {
+    s.misc_i[0] = -1;
+    s.misc_u[0] = 0;
+  }
+  __syncthreads();
+  uint32_t acc = ex;
+  for (int q = 0; q < per; ++q) {
+    int d = nb - 1 - per * t - q;
+    uint32_t h = H[d];
+    if (acc < need && need <= acc + h) {
+      s.misc_i[0] = d;
+      s.misc_u[0] = acc;
+    }
+    acc += h;
+  }
+  if (t == kThreads - 1 && incl < need) s.misc_u[1] = incl;
+  __syncthreads();
+  int d = s.misc_i[0];
+  *above = d >= 0 ? s.misc_u[0] : s.misc_u[1];
+  __syncthreads();
+  return d;
+}
+
+__device__ void clear_hist(uint32_t* H, int nb) {
+  for (int i = threadIdx.x; i < nb; i += kThreads) H[i] = 0;
+}
+
+// Ascending bitonic sort of a[0..n) in LDS, padded with ~0.
+__device__ void sort_u64_asc(uint64_t* a, uint32_t n) {
+  uint32_t np = 2;
+  while (np < n) np <<= 1;
+  for (uint32_t i = n + threadIdx.x; i < np; i += kThreads) a[i] = ~0ull;
+  __syncthreads();
+  for (uint32_t k = 2; k <= np; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t i = threadIdx.x; i < np; i += kThreads) {
+        uint32_t ixj = i ^ j;
+        if (ixj > i) {
+          uint64_t x = a[i], y = a[ixj];
+          bool up = (i & k) == 0;
+          if ((x > y) == up) {
+            a[i] = y;
+            a[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Wave-aggregated append into an LDS list; returns nothing, counts all.
+__device__ __forceinline__ void list_push(uint64_t* list, uint32_t* cnt, bool p, uint64_t val) {
+  unsigned long long m = __ballot(p);
+  if (!m) return;
+  const int lane = threadIdx.x & 63;
+  uint32_t base = 0;
+  int leader = __ffsll((long long)m) - 1;
+  if (lane == leader) base = atomicAdd(cnt, (uint32_t)__popcll(m));
+  base = __shfl(base, leader, 64);
+  if (p) {
+    uint32_t off = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+    if (off < (uint32_t)kCap) list[off] = val;
+  }
+}
+
+// ECSS over a row of V elements, x(i, v) for i < V; 16 contiguous elements
+// per thread per chunk.
+template <class X>
+__device__ EcssResult row_ecss(const Row& r, X&& xf, int mode, float theta, Smem& s) {
+  constexpr int M = 16;
+  const uint32_t V = r.V;
+  float c = 0.f;
+  for (uint32_t base = 0; base < V; base += (uint32_t)kThreads * M) {
+    const uint32_t i0 = base + threadIdx.x * M;
+    float x[M];
+#pragma unroll
+    for (int q = 0; q < M / 4; ++q) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      uint32_t i = i0 + 4 * q;
+      if (i < V) r.load4(i, v);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < V) ? xf(i + j, v[j]) : 0.f;
+    }
+    EcssResult e = ecss_chunk<M>(c, x, mode, theta, s.ecss);
+    if (e.found) {
+      e.pos += (int)base;
+      return e;
+    }
+    c = e.c;
+  }
+  EcssResult e;
+  e.c = c;
+  e.found = 0;
+  e.pos = -1;
+  e.before = 0.f;
+  return e;
+}
+
+// ECSS over n elements of an LDS-resident list, x(j) for j < n.
+template <int M, class X>
+__device__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
+  const uint32_t j0 = threadIdx.x * M;
+  float x[M];
+#pragma unroll
+  for (int q = 0; q < M; ++q) x[q] = (j0 + q < n) ? xf(j0 + q) : 0.f;
+  return ecss_chunk<M>(c0, x, mode, theta, s.ecss);
+}
+
+template <class X>
+__device__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
+  if (n <= 1024) return list_ecss_m<1>(n, xf, mode, theta, c0, s);
+  if (n <= 2048) return list_ecss_m<2>(n, xf, mode, theta, c0, s);
+  if (n <= 4096) return list_ecss_m<4>(n, xf, mode, theta, c0, s);
+  return list_ecss_m<8>(n, xf, mode, theta, c0, s);
+}
+
+// Walk over V tokens that all carry the same probability u (the uniform
+// branch of softmax, sampling.rs:211-214 and :224-227).
+__device__ EcssResult const_ecss(uint32_t V, float u, int mode, float theta, Smem& s) {
+  constexpr int M = 16;
+  float c = 0.f;
+  for (uint32_t base = 0; base < V; base += (uint32_t)kThreads * M) {
+    const uint32_t i0 = base + threadIdx.x * M;
+    float x[M];
+#pragma unroll
+    for (int j = 0; j < M; ++j) x[j] = (i0 + j < V) ? u : 0.f;
+    EcssResult e = ecss_chunk<M>(c, x, mode, theta, s.ecss);
+    if (e.found) {
+      e.pos += (int)base;
+      return e;
+    }
+    c = e.c;
+  }
+  EcssResult e;
+  e.c = c;
+  e.found = 0;
+  e.pos = -1;
+  e.before = 0.f;
+  return e;
+}
+
+__device__ __forceinline__ float penalize(float v, uint32_t count, const RowParams& P) {
+  // sampling.rs:881-900, one IEEE operation per step
+  float nv = v;
+  if (P.flags & kRep) nv = (v > 0.f) ? __fdiv_rn(v, P.rep) : __fmul_rn(v, P.rep);
+  nv = __fsub_rn(nv, P.presence);
+  nv = __fsub_rn(nv, __fmul_rn(P.freq, __uint2float_rn(count)));
+  return nv;
+}
+
+// --------------------------------------------------------------- the kernel
+
+struct Final {  // what the final stage needs to know about the list
+  uint32_t n;
+};
+
+__device__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrace& tr) {
+  if (threadIdx.x == 0) {
+    a.tokens[b] = token;
+    if (a.trace) {
+      tr.token = token;
+      a.trace[b] = tr;
+    }
+  }
+}
+
+// Final stage over the LDS list A (entries (idx << 32) | key, ascending idx,
+// n entries, every entry alive). Applies min-p, temperature, softmax, draw.
+__device__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint32_t n, float r,
+                                  Smem& s, RowTrace& tr) {
+  const uint32_t V = a.vocab;
+  auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
+  // min-p (sampling.rs:976-994)
+  bool mmask = false;
+  float bound = 0.f;
+  if (P.flags & kMinP) {
+    float m = kNegInf;
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) m = rmax(m, lv(j));
+    m = block_rmax(m, s);
+    if (is_finite(m)) {
+      mmask = true;
+      bound = __fadd_rn(m, P.log_min_p);
+    }
+  }
+  auto wv = [&](uint32_t j) -> float {
+    float v = lv(j);
+    if (mmask && v < bound) v = kNegInf;
+    return __fmul_rn(v, P.inv_temp);
+  };
+  float m3 = kNegInf;
+  uint32_t nan3 = 0;
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
+    float w = wv(j);
+    m3 = rmax(m3, w);
+    nan3 |= is_nan(w) ? 1u : 0u;
+  }
+  // tokens outside the list are -inf * inv_temp: they only matter when the
+  // list has no finite value at all (uniform branch over all V tokens)
+  m3 = block_rmax(m3, s);
+  nan3 = block_or_u32(nan3, s);
+  tr.final_max = m3;
+  if (!is_finite(m3)) {
+    tr.path |= 16u;
+    float u = __fdiv_rn(1.0f, __uint2float_rn(V));
+    EcssResult e = const_ecss(V, u, kEcssFindGt, r, s);
+    tr.final_sum = 0.f;
+    tr.cdf_before = e.found ? e.before : e.c;
+    tr.cdf_at = e.c;
+    return e.found ? (uint32_t)e.pos : V - 1;
+  }
+  if (nan3) {
+    // the sum is NaN, so every probability and every CDF value is NaN and the
+    // walk falls through to the last index (sampling.rs:1013)
+    tr.path |= 32u;
+    tr.final_sum = __uint_as_float(0x7fc00000u);
+    tr.cdf_before = tr.cdf_at = __uint_as_float(0x7fc00000u);
+    return V - 1;
+  }
+  EcssResult S = list_ecss(n, [&](uint32_t j) { return expf_glibc(__fsub_rn(wv(j), m3)); },
+                           kEcssSum, 0.f, 0.f, s);
+  const float S3 = S.c;
+  tr.final_sum = S3;
+  EcssResult e = list_ecss(
+      n, [&](uint32_t j) { return __fdiv_rn(expf_glibc(__fsub_rn(wv(j), m3)), S3); },
+      kEcssFindGt, r, 0.f, s);
+  tr.cdf_before = e.found ? e.before : e.c;
+  tr.cdf_at = e.c;
+  if (e.found) return (uint32_t)(s.A[e.pos] >> 32);
+  return V - 1;
+}
+
+extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs a) {
+  __shared__ Smem s;
+  const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
+  const uint32_t V = a.vocab;
+  RowTrace tr;
+  tr.status = 0; tr.path = 0; tr.topk_cutoff_key = 0; tr.topk_survivors = V; tr.topp_sum = 0.f;
+  tr.topp_kept = 0; tr.topp_cum = 0.f; tr.windows = 0; tr.final_max = 0.f; tr.final_sum = 0.f;
+  tr.cdf_before = 0.f; tr.cdf_at = 0.f; tr.token = 0; tr.passes = 0; tr.pad[0] = tr.pad[1] = 0;
+
+  Row row;
+  if (a.dtype == 0) {
+    row.f = reinterpret_cast<const float*>(a.logits) + (uint64_t)b * a.row_stride;
+    row.h = nullptr;
+    row.vec = ((reinterpret_cast<uintptr_t>(row.f) & 15u) == 0);
+  } else {
+    row.f = nullptr;
+    row.h = reinterpret_cast<const uint16_t*>(a.logits) + (uint64_t)b * a.row_stride;
+    row.vec = ((reinterpret_cast<uintptr_t>(row.h) & 7u) == 0);
+  }
+  row.V = V;
+
+  // ---- penalties: materialize the penalized row (sampling.rs:850-879) ----
+  const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+  if ((P.flags & kPen) && h1 > h0) {
+    float* dst = a.pen_scratch + (uint64_t)b * a.pen_stride;
+    row_foreach(row, [&](uint32_t i, float v) { dst[i] = v; });
+    __syncthreads();
+    for (uint32_t j = h0 + t; j < h1; j += kThreads) {
+      uint32_t id = a.hist_ids[j];
+      if (id < V) dst[id] = penalize(row.at(id), a.hist_cnt[j], P);
+    }
+    __syncthreads();
+    row.f = dst;
+    row.h = nullptr;
+    row.vec = true;
+    tr.passes++;
+  }
+  if (a.pen_out) {
+    float* po = a.pen_out + (uint64_t)b * V;
+    row_foreach(row, [&](uint32_t i, float v) { po[i] = v; });
+  }
+
+  // ---- greedy (sampling.rs:468-476) ----
+  if (P.flags & kGreedy) {
+    uint64_t best = 0;
+    row_foreach(row, [&](uint32_t i, float v) {
+      uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+      best = k > best ? k : best;
+    });
+    best = block_max_u64(best, s);
+    tr.path |= 1u;
+    tr.passes++;
+    write_result(a, b, 0xffffffffu - (uint32_t)best, tr);
+    return;
+  }
+
+  const float rdraw = a.inline_rows ? a.inline_uniforms[b] : a.uniforms[b];
+  bool small = false;   // survivors in s.A as (idx << 32) | key, ascending idx
+  uint32_t nlist = 0;
+  bool topp_done = false;
+  bool kmask = false;   // large path with a top-k cutoff mask
+  uint32_t kcut = 0;
+
+  // ---- top-k (sampling.rs:904-933) ----
+  if (P.flags & kTopK) {
+    const uint32_t k = P.top_k;
+    if (k == 1) {
+      uint64_t best = 0;
+      row_foreach(row, [&](uint32_t i, float v) {
+        uint64_t kk = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+        best = kk > best ? kk : best;
+      });
+      best = block_max_u64(best, s);
+      tr.passes++;
+      const uint32_t idx = 0xffffffffu - (uint32_t)best, key = (uint32_t)(best >> 32);
+      if (t == 0) s.A[0] = ((uint64_t)idx << 32) | key;
+      __syncthreads();
+      nlist = 1;
+      small = true;
+      tr.topk_cutoff_key = key;
+      tr.topk_survivors = 1;
+    } else {
+      uint32_t prefix = 0, pmask = 0, above = 0;
+      for (int lvl = 0; lvl < 3 && !small; ++lvl) {
+        const int sh = lvl == 0 ? 21 : (lvl == 1 ? 10 : 0);
+        const int nb = lvl == 2 ? 1024 : 2048;
+        const uint32_t dm = (uint32_t)nb - 1u;
+        clear_hist(s.H, nb);
+        __syncthreads();
+        row_foreach(row, [&](uint32_t i, float v) {
+          uint32_t kk = tkey(v);
+          if ((kk & pmask) == prefix) atomicAdd(&s.H[(kk >> sh) & dm], 1u);
+        });
+        __syncthreads();
+        tr.passes++;
+        uint32_t ab = 0;
+        int d = find_from_top(s.H, nb, k - above, &ab, s);
+        above += ab;
+        prefix |= (uint32_t)d << sh;
+        pmask |= dm << sh;
+        const uint32_t cnt_ge = above + s.H[d];
+        __syncthreads();
+        if (cnt_ge <= (uint32_t)kCap) {
+          // compact all keys >= prefix (the smallest key on this digit path)
+          if (t == 0) s.cnt = 0;
+          __syncthreads();
+          row_foreach(row, [&](uint32_t i, float v) {
+            uint32_t kk = tkey(v);
+            list_push(s.A, &s.cnt, kk >= prefix, ((uint64_t)(~kk) << 32) | i);
+          });
+          __syncthreads();
+          tr.passes++;
+          const uint32_t n = s.cnt;
+          sort_u64_asc(s.A, n);  // descending key
+          const uint32_t cut = ~(uint32_t)(s.A[k - 1] >> 32);
+          // survivors: every entry with key >= cut is a prefix of the list
+          uint32_t ns = 0;
+          for (uint32_t j = t; j < n; j += kThreads) ns += (~(uint32_t)(s.A[j] >> 32) >= cut) ? 1u : 0u;
+          ns = block_sum_u32(ns, s);
+          for (uint32_t j = t; j < ns; j += kThreads) {
+            uint64_t e = s.A[j];
+            s.A[j] = ((uint64_t)(uint32_t)e << 32) | (uint64_t)(~(uint32_t)(e >> 32));
+          }
+          __syncthreads();
+          sort_u64_asc(s.A, ns);  // ascending index
+          nlist = ns;
+          small = true;
+          tr.topk_cutoff_key = cut;
+          tr.topk_survivors = ns;
+        } else if (lvl == 2) {
+          kmask = true;
+          kcut = prefix;
+          tr.topk_cutoff_key = prefix;
+          tr.topk_survivors = cnt_ge;
+        }
+      }
+    }
+  }
+
+  // value after the top-k mask (large path)
+  auto v1f = [&](float v) -> float { return (kmask && tkey(v) < kcut) ? kNegInf : v; };
+
+  int pmode = 0;        // 0 none, 1 uniform index prefix, 2 probability threshold
+  uint32_t plim = 0;    // pmode 1: keep idx <= plim
+  float m1 = 0.f, S1 = 1.f, pstar = 0.f;
+  uint32_t istar = 0;   // pmode 2: keep p > pstar or (p == pstar and idx <= istar)
+
+  if (!small) tr.path |= 4u;
+
+  // ---- top-p on the large path (sampling.rs:942-967) ----
+  if ((P.flags & kTopP) && !small) {
+    float m = kNegInf;
+    uint32_t nan = 0;
+    row_foreach(row, [&](uint32_t i, float v) {
+      float x = v1f(v);
+      m = rmax(m, x);
+      nan |= is_nan(x) ? 1u : 0u;
+    });
+    m = block_rmax(m, s);
+    nan = block_or_u32(nan, s);
+    tr.passes++;
+    m1 = m;
+    topp_done = true;
+    if (!is_finite(m1)) {
+      tr.path |= 8u;
+      float u = __fdiv_rn(1.0f, __uint2float_rn(V));
+      EcssResult e = const_ecss(V, u, kEcssFindGe, P.top_p, s);
+      tr.topp_sum = 0.f;
+      if (e.found) {
+        pmode = 1;
+        plim = (uint32_t)e.pos;
+        tr.topp_kept = plim + 1;
+      } else {
+        tr.topp_kept = V;
+      }
+      tr.topp_cum = e.c;
+    } else if (nan) {
+      tr.topp_sum = __uint_as_float(0x7fc00000u);
+      tr.topp_kept = V;
+    } else {
+      // softmax sum at T = 1 and a key histogram of the positive-probability tokens
+      clear_hist(s.H0, 2048);
+      __syncthreads();
+      EcssResult e = row_ecss(
+          row,
+          [&](uint32_t i, float v) {
+            float x = expf_glibc(__fsub_rn(v1f(v), m1));
+            if (x > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
+            return x;
+          },
+          kEcssSum, 0.f, s);
+      __syncthreads();
+      tr.passes++;
+      S1 = e.c;
+      tr.topp_sum = S1;
+      // walk the probability order window by window
+      uint64_t key_hi = 1ull << 32;
+      float p_hi = __uint_as_float(0x7f800000u);
+      float c = 0.f;
+      uint32_t ranks = 0;
+      bool found = false;
+      for (;;) {
+        // plan the next window [L, key_hi) of at most kCapWindow keys
+        uint32_t L = 0;
+        bool empty = false, overflow = false;
+        {
+          uint32_t pre = 0, pm = 0;
+          bool decided = false;
+          for (int lvl = 0; lvl < 3 && !decided; ++lvl) {
+            const int sh = lvl == 0 ? 21 : (lvl == 1 ? 10 : 0);
+            const int nb = lvl == 2 ? 1024 : 2048;
+            const uint32_t dm = (uint32_t)nb - 1u;
+            uint32_t* H = s.H;
+            if (lvl == 0 && (key_hi & 0x1fffffull) == 0) {
+              // level-0 counts of the remaining keys come from the saved histogram
+              const uint32_t top = (uint32_t)(key_hi >> 21);
+              for (int i = t; i < 2048; i += kThreads) s.H[i] = (uint32_t)i < top ? s.H0[i] : 0u;
+              __syncthreads();
+            } else {
+              clear_hist(H, nb);
+              __syncthreads();
+              const float lo_cut = __fsub_rn(m1, 104.f);
+              row_foreach(row, [&](uint32_t i, float v) {
+                float x = v1f(v);
+                uint32_t kk = tkey(x);
+                if ((uint64_t)kk < key_hi && (kk & pm) == pre && x >= lo_cut)
+                  atomicAdd(&H[(kk >> sh) & dm], 1u);
+              });
+              __syncthreads();
+              tr.passes++;
+            }
+            uint32_t ab = 0;
+            int d = find_from_top(H, nb, (uint32_t)kCapWindow + 1u, &ab, s);
+            if (d < 0) {
+              // everything that remains under this prefix fits
+              if (ab == 0 && lvl == 0) empty = true;
+              L = pre;
+              decided = true;
+            } else if (ab > 0) {
+              L = pre | (((uint32_t)d + 1u) << sh);
+              decided = true;
+            } else {
+              pre |= (uint32_t)d << sh;
+              pm |= dm << sh;
+            }
+            __syncthreads();
+          }
+          if (!decided) overflow = true;  // more than a window of one exact key
+        }
+        if (empty) break;
+        if (!overflow && (uint64_t)L >= key_hi) overflow = true;  // no progress: never loop
+        if (overflow || tr.windows >= 4096u) {
+          tr.status = kStatusTieOverflow;
+          break;
+        }
+        // probability window [p_lo, p_hi)
+        const float vL = key2f(L);
+        const float p_lo = (L == 0u) ? 0.f : __fdiv_rn(expf_glibc(__fsub_rn(vL, m1)), S1);
+        const float vH = key_hi >= (1ull << 32) ? __uint_as_float(0x7f800000u) : key2f((uint32_t)key_hi);
+        const float dl = __fadd_rn(__fmul_rn(fabsf(vL) + fabsf(m1), 0x1p-12f), 0x1p-20f);
+        const float dh = __fadd_rn(__fmul_rn(fabsf(vH) + fabsf(m1), 0x1p-12f), 0x1p-20f);
+        const float lo_v = (L == 0u) ? kNegInf : __fsub_rn(vL, dl);
+        const float hi_v = __fadd_rn(vH, dh);
+        if (t == 0) s.cnt = 0;
+        __syncthreads();
+        row_foreach(row, [&](uint32_t i, float v) {
+          float x = v1f(v);
+          bool in = false;
+          uint32_t pb = 0;
+          if (x >= lo_v && x <= hi_v) {
+            float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
+            in = p > 0.f && p >= p_lo && p < p_hi;
+            pb = __float_as_uint(p);
+          }
+          list_push(s.Bk, &s.cnt, in, ((uint64_t)(~pb) << 32) | i);
+        });
+        __syncthreads();
+        tr.passes++;
+        const uint32_t n = s.cnt;
+        if (n > (uint32_t)kCap) {
+          tr.status = kStatusListOverflow;
+          break;
+        }
+        tr.windows++;
+        sort_u64_asc(s.Bk, n);
+        EcssResult w = list_ecss(
+            n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); },
+            kEcssFindGe, P.top_p, c, s);
+        if (w.found) {
+          found = true;
+          pstar = __uint_as_float(~(uint32_t)(s.Bk[w.pos] >> 32));
+          istar = (uint32_t)s.Bk[w.pos];
+          tr.topp_kept = ranks + (uint32_t)w.pos + 1u;
+          tr.topp_cum = w.c;
+          if (tr.windows == 1) {
+            // the whole nucleus is in LDS: continue on the small path
+            const uint32_t nk = (uint32_t)w.pos + 1u;
+            for (uint32_t j = t; j < nk; j += kThreads) {
+              uint32_t idx = (uint32_t)s.Bk[j];
+              s.A[j] = ((uint64_t)idx << 32) | tkey(v1f(row.at(idx)));
+            }
+            __syncthreads();
+            sort_u64_asc(s.A, nk);
+            nlist = nk;
+            small = true;
+          } else {
+            pmode = 2;
+          }
+          break;
+        }
+        c = w.c;
+        ranks += n;
+        if (L == 0u) break;
+        key_hi = L;
+        p_hi = p_lo;
+      }
+      if (!found) {
+        tr.topp_kept = V;
+        tr.topp_cum = c;
+      }
+      if (tr.status) {
+        write_result(a, b, 0xffffffffu, tr);
+        return;
+      }
+    }
+  }
+
+  if (small) {
+    tr.path |= 2u;
+    // top-p on the list (sampling.rs:942-967)
+    bool lpred = false;  // list-level top-p predicate active
+    bool lunif = false;
+    uint32_t lplim = 0;
+    float lpstar = 0.f, lm1 = 0.f, lS1 = 1.f;
+    uint32_t ljstar = 0;
+    const uint32_t n = nlist;
+    auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
+    if ((P.flags & kTopP) && !topp_done) {
+      float m = kNegInf;
+      uint32_t nan = 0;
+      for (uint32_t j = t; j < n; j += kThreads) {
+        m = rmax(m, lv(j));
+        nan |= is_nan(lv(j)) ? 1u : 0u;
+      }
+      m = block_rmax(m, s);
+      nan = block_or_u32(nan, s);
+      lm1 = m;
+      if (!is_finite(m)) {
+        tr.path |= 8u;
+        float u = __fdiv_rn(1.0f, __uint2float_rn(V));
+        EcssResult e = const_ecss(V, u, kEcssFindGe, P.top_p, s);
+        if (e.found) {
+          lunif = true;
+          lplim = (uint32_t)e.pos;
+          tr.topp_kept = lplim + 1;
+        } else {
+          tr.topp_kept = V;
+        }
+        tr.topp_cum = e.c;
+      } else if (nan) {
+        tr.topp_sum = __uint_as_float(0x7fc00000u);
+        tr.topp_kept = V;
+      } else {
+        EcssResult e = list_ecss(
+            n, [&](uint32_t j) { return expf_glibc(__fsub_rn(lv(j), lm1)); }, kEcssSum, 0.f, 0.f, s);
+        lS1 = e.c;
+        tr.topp_sum = lS1;
+        for (uint32_t j = t; j < n; j += kThreads) {
+          float p = __fdiv_rn(expf_glibc(__fsub_rn(lv(j), lm1)), lS1);
+          s.Bk[j] = ((uint64_t)(~__float_as_uint(p)) << 32) | j;
+        }
+        __syncthreads();
+        sort_u64_asc(s.Bk, n);
+        EcssResult w = list_ecss(
+            n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); },
+            kEcssFindGe, P.top_p, 0.f, s);
+        if (w.found) {
+          lpred = true;
+          lpstar = __uint_as_float(~(uint32_t)(s.Bk[w.pos] >> 32));
+          ljstar = (uint32_t)s.Bk[w.pos];
+          tr.topp_kept = (uint32_t)w.pos + 1u;
+        } else {
+          tr.topp_kept = V;
+        }
+        tr.topp_cum = w.c;
+      }
+    }
+    // compact the list to the entries that survive top-p
+    if (lpred || lunif) {
+      if (t == 0) s.cnt = 0;
+      __syncthreads();
+      // entries are kept in index order: process in order with a block scan
+      for (uint32_t base = 0; base < n; base += kThreads) {
+        const uint32_t j = base + t;
+        bool keep = false;
+        uint64_t e = 0;
+        if (j < n) {
+          e = s.A[j];
+          if (lunif) {
+            keep = (uint32_t)(e >> 32) <= lplim;
+          } else {
+            float p = __fdiv_rn(expf_glibc(__fsub_rn(lv(j), lm1)), lS1);
+            keep = p > lpstar || (p == lpstar && j <= ljstar);
+          }
+        }
+        uint32_t inc = block_incl_scan_u32(keep ? 1u : 0u, s);
+        const uint32_t c0 = s.cnt;
+        __syncthreads();
+        if (keep) s.Bk[c0 + inc - 1] = e;
+        if (t == kThreads - 1) s.cnt = c0 + inc;
+        __syncthreads();
+      }
+      const uint32_t nk = s.cnt;
+      for (uint32_t j = t; j < nk; j += kThreads) s.A[j] = s.Bk[j];
+      __syncthreads();
+      nlist = nk;
+    }
+    uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr);
+    write_result(a, b, tok, tr);
+    return;
+  }
+
+  // ---- large path: min-p, temperature, softmax, draw over the whole row ----
+  auto v2f = [&](uint32_t i, float v) -> float {
+    float x = v1f(v);
+    if (pmode == 1) {
+      if (i > plim) x = kNegInf;
+    } else if (pmode == 2) {
+      float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
+      if (!(p > pstar || (p == pstar && i <= istar))) x = kNegInf;
+    }
+    return x;
+  };
+  bool mmask = false;
+  float bound = 0.f;
+  if (P.flags & kMinP) {
+    float m = kNegInf;
+    row_foreach(row, [&](uint32_t i, float v) { m = rmax(m, v2f(i, v)); });
+    m = block_rmax(m, s);
+    tr.passes++;
+    if (is_finite(m)) {
+      mmask = true;
+      bound = __fadd_rn(m, P.log_min_p);
+    }
+  }
+  auto wf = [&](uint32_t i, float v) -> float {
+    float x = v2f(i, v);
+    if (mmask && x < bound) x = kNegInf;
+    return __fmul_rn(x, P.inv_temp);
+  };
+  float m3 = kNegInf;
+  uint32_t nan3 = 0;
+  row_foreach(row, [&](uint32_t i, float v) {
+    float w = wf(i, v);
+    m3 = rmax(m3, w);
+    nan3 |= is_nan(w) ? 1u : 0u;
+  });
+  m3 = block_rmax(m3, s);
+  nan3 = block_or_u32(nan3, s);
+  tr.passes++;
+  tr.final_max = m3;
+  uint32_t tok;
+  if (!is_finite(m3)) {
+    tr.path |= 16u;
+    float u = __fdiv_rn(1.0f, __uint2float_rn(V));
+    EcssResult e = const_ecss(V, u, kEcssFindGt, rdraw, s);
+    tr.cdf_before = e.found ? e.before : e.c;
+    tr.cdf_at = e.c;
+    tok = e.found ? (uint32_t)e.pos : V - 1;
+  } else if (nan3) {
+    tr.path |= 32u;
+    tr.final_sum = __uint_as_float(0x7fc00000u);
+    tr.cdf_before = tr.cdf_at = __uint_as_float(0x7fc00000u);
+    tok = V - 1;
+  } else {
+    EcssResult S = row_ecss(
+        row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, kEcssSum,
+        0.f, s);
+    tr.passes++;
+    const float S3 = S.c;
+    tr.final_sum = S3;
+    EcssResult e = row_ecss(
+        row,
+        [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
+        kEcssFindGt, rdraw, s);
+    tr.passes++;
+    tr.cdf_before = e.found ? e.before : e.c;
+    tr.cdf_at = e.c;
+    tok = e.found ? (uint32_t)e.pos : V - 1;
+  }
+  write_result(a, b, tok, tr);
+}
+
+}  // namespace lumen

@@ -1,0 +1,263 @@
+"""Host-side mirror of Lumen's sampler API over the gfx950 engine.
+
+Same names, argument meaning and behaviour as
+crates/lumen-runtime/src/sampling.rs:
+  SamplingParams (:239-338), Xorshift64 (:45-106), SamplerState (:352-393),
+  Sampler (:397-434), sample_logits (:452-527),
+plus the engine shims sample_token / sample_token_with_state
+(crates/lumen-runtime/src/engine.rs:61-88).
+
+Logits are device tensors (torch, fp32 or bf16, on the GPU). They are never
+modified (the reference overwrites its slice; callers must not rely on that
+either way). Every call goes through liblumen_sampler.so; there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+from . import _native
+
+F32_EPSILON = float(np.finfo(np.float32).eps)
+
+
+@dataclass
+class SamplingParams:
+    """sampling.rs:239-325. `None` behaves exactly like the reference's None."""
+
+    temperature: float = 1.0
+    seed: Optional[int] = None
+    top_p: Optional[float] = None
+    top_k: Optional[int] = None
+    min_p: Optional[float] = None
+    repetition_penalty: Optional[float] = None
+    presence_penalty: Optional[float] = None
+    frequency_penalty: Optional[float] = None
+    repeat_last_n: Optional[int] = None
+    anti_restate: bool = False
+
+    def penalties_active(self) -> bool:
+        """sampling.rs:332-337 (f32 arithmetic)."""
+        rep = np.float32(1.0 if self.repetition_penalty is None else self.repetition_penalty)
+        presence = np.float32(self.presence_penalty or 0.0)
+        freq = np.float32(self.frequency_penalty or 0.0)
+        return bool(abs(np.float32(rep - np.float32(1.0))) >= np.float32(F32_EPSILON)
+                    or presence != 0.0 or freq != 0.0)
+
+    def to_c(self) -> _native.SamplingParamsC:
+        return _native.SamplingParamsC(
+            float(self.temperature),
+            float(1.0 if self.top_p is None else self.top_p),
+            float(0.0 if self.min_p is None else self.min_p),
+            float(1.0 if self.repetition_penalty is None else self.repetition_penalty),
+            float(0.0 if self.presence_penalty is None else self.presence_penalty),
+            float(0.0 if self.frequency_penalty is None else self.frequency_penalty),
+            int(self.top_k or 0),
+            int(self.repeat_last_n or 0),
+            int(bool(self.anti_restate)),
+            0,
+        )
+
+
+class Xorshift64:
+    """sampling.rs:45-106, through the library's C implementation."""
+
+    def __init__(self, seed: int):
+        self._state = ctypes.c_uint64(_native.load().lumen_xorshift64_new(seed & (2**64 - 1)))
+
+    @classmethod
+    def new(cls, seed: int) -> "Xorshift64":
+        return cls(seed)
+
+    def next_u64(self) -> int:
+        return _native.load().lumen_xorshift64_next_u64(ctypes.byref(self._state))
+
+    def next_f32(self) -> float:
+        return _native.load().lumen_xorshift64_next_f32(ctypes.byref(self._state))
+
+    def state(self) -> int:
+        return self._state.value
+
+    def set_state(self, s: int):
+        self._state.value = s
+
+
+@dataclass
+class SamplerState:
+    """sampling.rs:352-393: history and per-token counts."""
+
+    history: List[int] = field(default_factory=list)
+    freq: Dict[int, int] = field(default_factory=dict)
+
+    def record(self, token: int):
+        self.history.append(int(token))
+        self.freq[int(token)] = self.freq.get(int(token), 0) + 1
+
+    def clear(self):
+        self.history.clear()
+        self.freq.clear()
+
+
+def _as_device_logits(logits):
+    import torch
+
+    if not isinstance(logits, torch.Tensor) or not logits.is_cuda:
+        raise TypeError("logits must be a GPU torch.Tensor (fp32 or bf16)")
+    if logits.dtype == torch.float32:
+        dt = _native.DTYPE_F32
+    elif logits.dtype == torch.bfloat16:
+        dt = _native.DTYPE_BF16
+    else:
+        raise TypeError(f"unsupported logits dtype {logits.dtype}")
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [B, V] with unit stride along V")
+    return logits, dt
+
+
+class Engine:
+    """One lumen_sampler context on one GPU (the C-ABI object)."""
+
+    def __init__(self, device: int = 0):
+        L = _native.load()
+        h = ctypes.c_void_p()
+        _native.check(L.lumen_sampler_create(ctypes.byref(h), int(device)), "lumen_sampler_create")
+        self._h = h
+        self.device = device
+
+    def close(self):
+        if self._h:
+            _native.load().lumen_sampler_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sample_batch(self, logits, params: Sequence[SamplingParams],
+                     histories: Optional[Sequence[Sequence[int]]] = None,
+                     uniforms: Optional[Sequence[float]] = None,
+                     rngs: Optional[Sequence[Xorshift64]] = None,
+                     penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
+                     sync: bool = True, stream=None):
+        """Samples every row of `logits` [B, V].
+
+        histories: SamplerState.history per row (the window is applied here),
+        or penalty_counts = (offsets, ids, counts) device int32 tensors already
+        windowed (the caller-resident SamplerState.freq).
+        uniforms: one draw per row; or rngs: Xorshift64 per row (advanced).
+        Returns the token tensor (device); with sync=True also a host list.
+        """
+        import torch
+
+        L = _native.load()
+        lg, dt = _as_device_logits(logits)
+        B, V = lg.shape
+        if len(params) != B:
+            raise ValueError("one SamplingParams per row")
+        pc = (_native.SamplingParamsC * B)(*[p.to_c() for p in params])
+        bt = _native.BatchC()
+        bt.logits = lg.data_ptr()
+        bt.dtype = dt
+        bt.batch = B
+        bt.vocab = V
+        bt.row_stride = lg.stride(0) if B > 1 else V  # a size-1 dim may carry any stride
+        bt.params = pc
+        keep = []
+        if penalty_counts is not None:
+            offs, ids, cnts = penalty_counts
+            bt.pen_offsets = offs.data_ptr()
+            bt.pen_ids = ids.data_ptr()
+            bt.pen_counts = cnts.data_ptr()
+        elif histories is not None:
+            offs = np.zeros(B + 1, dtype=np.uint64)
+            offs[1:] = np.cumsum([len(h) for h in histories])
+            flat = np.concatenate([np.asarray(h, dtype=np.uint32).reshape(-1) for h in histories]
+                                  + [np.zeros(1, np.uint32)])
+            keep += [offs, flat]
+            bt.history_offsets = offs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
+            bt.history = flat.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+        if rngs is not None:
+            st = np.array([r.state() for r in rngs], dtype=np.uint64)
+            keep.append(st)
+            bt.rng_states = st.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
+        else:
+            u = np.zeros(B, dtype=np.float32) if uniforms is None else \
+                np.ascontiguousarray(uniforms, dtype=np.float32)
+            keep.append(u)
+            bt.uniforms = u.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        dev = lg.device
+        if tokens_out is None:
+            tokens_out = torch.empty(B, dtype=torch.int32, device=dev)
+        bt.tokens = tokens_out.data_ptr()
+        if trace is not None:
+            bt.trace = trace.data_ptr()
+        if penalized_out is not None:
+            bt.penalized_out = penalized_out.data_ptr()
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        if sync:
+            host = (ctypes.c_uint32 * B)()
+            rc = L.lumen_sampler_sample_batch_sync(self._h, ctypes.byref(bt), host, s)
+        else:
+            rc = L.lumen_sampler_sample_batch(self._h, ctypes.byref(bt), s)
+        if rngs is not None:
+            for r, v in zip(rngs, st.tolist()):
+                r.set_state(int(v))
+        _native.check(rc, "lumen_sampler_sample_batch")
+        return (tokens_out, list(host)) if sync else (tokens_out, None)
+
+
+_engines: Dict[int, Engine] = {}
+
+
+def engine(device: int = 0) -> Engine:
+    if device not in _engines:
+        _engines[device] = Engine(device)
+    return _engines[device]
+
+
+def sample_logits(logits, params: SamplingParams, state: SamplerState, rng: Xorshift64) -> int:
+    """sampling.rs:452-527 for one row; does not record (as the reference)."""
+    dev = logits.device.index or 0
+    if logits.numel() == 0:
+        return 0
+    _, toks = engine(dev).sample_batch(logits, [params], histories=[state.history], rngs=[rng])
+    return int(toks[0])
+
+
+class Sampler:
+    """sampling.rs:397-434."""
+
+    def __init__(self, params: SamplingParams, rng: Optional[Xorshift64] = None):
+        self.params = params
+        self.state = SamplerState()
+        self.rng = rng if rng is not None else Xorshift64(42 if params.seed is None
+                                                          else params.seed)
+
+    @classmethod
+    def with_rng(cls, params: SamplingParams, rng: Xorshift64) -> "Sampler":
+        return cls(params, rng)
+
+    def sample(self, logits) -> int:
+        token = sample_logits(logits, self.params, self.state, self.rng)
+        self.state.record(token)
+        return token
+
+
+def sample_token(logits, params: SamplingParams, rng: Xorshift64) -> int:
+    """engine.rs:61-70: transient empty state."""
+    return sample_logits(logits, params, SamplerState(), rng)
+
+
+def sample_token_with_state(logits, params: SamplingParams, state: SamplerState,
+                            rng: Xorshift64) -> int:
+    """engine.rs:80-88: samples then records."""
+    t = sample_logits(logits, params, state, rng)
+    state.record(t)
+    return t

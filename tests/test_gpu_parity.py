@@ -1,0 +1,250 @@
+"""GPU parity: the gfx950 engine against the CPU oracle, through the C ABI.
+
+Bar: token ids, top-k cutoff and survivor counts, penalized logits and every
+intermediate f32 sum (top-p softmax sum, final softmax sum, the CDF value at
+the draw) must be bit-identical to the oracle's.
+"""
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+from lumen_amd.sampling import SamplingParams as SP  # noqa: E402
+from tests import parity  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    from lumen_amd.sampling import Engine
+
+    e = Engine(0)
+    yield e
+    e.close()
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def assert_clean(rep, name):
+    msg = f"{name}: tokens {rep['token_mismatch'][:5]} trace {rep['trace_mismatch'][:3]} " \
+          f"pen {rep['pen_mismatch'][:3]} status {set(rep['status'])}"
+    assert not rep["token_mismatch"], msg
+    assert not rep["trace_mismatch"], msg
+    assert not rep["pen_mismatch"], msg
+    assert set(rep["status"]) <= {0}, msg
+
+
+def run_case(eng, logits, params, hists=None, uniforms=None, name="case", **kw):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    if logits.ndim == 1:
+        logits = logits[None, :]
+    B = logits.shape[0]
+    if hists is None:
+        hists = [np.zeros(0, np.uint32)] * B
+    if uniforms is None:
+        rng = np.random.default_rng(abs(hash(name)) % 2**32)
+        uniforms = rng.random(B).astype(np.float32)
+    log(f"case {name} B={B} V={logits.shape[1]}")
+    rep = parity.compare(eng, logits, params, hists, uniforms, **kw)
+    assert_clean(rep, name)
+    return rep
+
+
+# ---- the reference's own small cases, on the GPU ---------------------------
+
+def test_reference_small_cases(eng):
+    cases = [
+        ([1.0, 5.0, 3.0, 2.0], SP(temperature=0.0), []),
+        ([0.0, 0.0, 0.0, 9.0, 9.0, 9.0], SP(temperature=0.0), []),
+        ([7.0, 7.0, 7.0, 7.0], SP(temperature=0.0), []),
+        ([1.0, 5.0, 3.0, 2.0], SP(temperature=0.0, top_p=0.5, top_k=1, min_p=0.9,
+                                  repetition_penalty=2.0, presence_penalty=10.0,
+                                  frequency_penalty=10.0), [1]),
+        ([3.0, 3.5], SP(temperature=0.0, frequency_penalty=10.0, repeat_last_n=2), [0, 0, 1, 1]),
+        ([3.0, 3.5], SP(temperature=0.0, frequency_penalty=10.0, repeat_last_n=1), [0, 0, 0, 1]),
+        ([1.0, 5.0, 3.0, 2.0, 4.0], SP(temperature=1.0, top_k=1), []),
+        ([1.0, 2.0, 2.0, 0.5], SP(temperature=1.0, top_k=1), []),
+        ([0.0, 0.0, 0.0, 10.0], SP(temperature=1.0, top_p=0.5), []),
+        ([0.0, 0.0, 0.0, 10.0], SP(temperature=1.0, min_p=0.5), []),
+        ([3.0, 2.0, 1.0, 0.5], SP(temperature=1.0, top_p=0.6, top_k=2, repetition_penalty=10.0), [3]),
+        ([4.0, 3.0, 2.0, 1.0], SP(temperature=0.5, top_p=0.85), []),
+        ([5.0, 2.0, 1.0, 0.0], SP(temperature=1.0, min_p=0.1), []),
+        ([-5.0, 5.0, 0.0, 0.0], SP(temperature=1.0), []),
+        ([1.0, 1.0], SP(temperature=1.0, repetition_penalty=10.0), [0]),
+    ]
+    for i, (lg, p, h) in enumerate(cases):
+        for r in (0.0, 0.1, 0.5, 0.73, 0.999):
+            run_case(eng, np.array(lg, np.float32), [p], [np.array(h, np.uint32)],
+                     np.array([r], np.float32), name=f"ref{i}_r{r}", check_pen=True)
+
+
+def test_determinism_sin_logits(eng):
+    base = np.sin(np.arange(1000, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    B = 32
+    lg = np.tile(base, (B, 1))
+    rng = np.random.default_rng(7)
+    params = [SP(temperature=0.7, top_p=0.9, top_k=40)] * B
+    run_case(eng, lg, params, uniforms=rng.random(B).astype(np.float32), name="sin1000")
+
+
+# ---- randomized small-V sweep over the parameter surface --------------------
+
+def random_params(rng, V):
+    T = float(rng.choice([0.0, 0.0, 0.3, 0.7, 1.0, 1.5, 1e-3]))
+    p = SP(temperature=T)
+    if rng.random() < 0.5:
+        p.top_k = int(rng.choice([1, 2, 3, 5, 40, V - 1, V, V + 5]))
+    if rng.random() < 0.5:
+        p.top_p = float(rng.choice([0.1, 0.5, 0.9, 0.95, 0.999, 1.0]))
+    if rng.random() < 0.3:
+        p.min_p = float(rng.choice([0.01, 0.1, 0.5]))
+    if rng.random() < 0.4:
+        p.repetition_penalty = float(rng.choice([1.05, 1.1, 2.0, 0.9]))
+    if rng.random() < 0.3:
+        p.presence_penalty = float(rng.choice([0.5, 1.5, -0.3]))
+    if rng.random() < 0.3:
+        p.frequency_penalty = float(rng.choice([0.25, 0.8]))
+    if rng.random() < 0.2:
+        p.repeat_last_n = int(rng.choice([1, 4, 64]))
+    return p
+
+
+def random_logits(rng, V, style):
+    if style == 0:
+        return rng.normal(0, 3, V).astype(np.float32)
+    if style == 1:  # heavy ties
+        return (np.round(rng.normal(0, 2, V) * 4) / 4).astype(np.float32)
+    if style == 2:  # very peaked
+        x = rng.normal(0, 1, V).astype(np.float32)
+        x[rng.integers(0, V)] += 40
+        return x
+    if style == 3:  # with -inf holes
+        x = rng.normal(0, 2, V).astype(np.float32)
+        x[rng.random(V) < 0.3] = -np.inf
+        return x
+    if style == 4:  # flat
+        return rng.normal(0, 0.1, V).astype(np.float32)
+    return rng.uniform(-100, 100, V).astype(np.float32)
+
+
+@pytest.mark.parametrize("V", [1, 2, 3, 17, 64, 1000, 4099])
+def test_random_small_vocab(eng, V):
+    rng = np.random.default_rng(V)
+    B = 48
+    lg = np.stack([random_logits(rng, V, b % 6) for b in range(B)])
+    params = [random_params(rng, V) for _ in range(B)]
+    hists = [rng.integers(0, V + 3, int(rng.integers(0, 40))).astype(np.uint32) for _ in range(B)]
+    run_case(eng, lg, params, hists, rng.random(B).astype(np.float32), name=f"rand{V}",
+             check_pen=True)
+
+
+def test_special_values(eng):
+    V = 300
+    rows, params = [], []
+    nan = np.float32(np.nan)
+    mk = []
+    x = np.zeros(V, np.float32); x[5] = np.inf; mk.append(x)
+    x = np.full(V, -np.inf, np.float32); mk.append(x)
+    x = np.zeros(V, np.float32); x[7] = nan; mk.append(x)
+    x = np.linspace(-1, 1, V).astype(np.float32); x[9] = nan; x[10] = np.inf; mk.append(x)
+    x = np.zeros(V, np.float32); x[3] = -0.0; mk.append(x)
+    x = np.full(V, 3.0, np.float32); mk.append(x)
+    x = np.linspace(-200, 0, V).astype(np.float32); mk.append(x)
+    neg_nan = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+    x = np.zeros(V, np.float32); x[11] = neg_nan; mk.append(x)
+    for x in mk:
+        for p in (SP(temperature=0.0), SP(temperature=1.0), SP(temperature=1.0, top_k=5),
+                  SP(temperature=0.8, top_p=0.9), SP(temperature=1.0, top_k=1),
+                  SP(temperature=2.0, min_p=0.2), SP(temperature=1.0, top_k=10, top_p=0.5)):
+            rows.append(x)
+            params.append(p)
+    lg = np.stack(rows)
+    rng = np.random.default_rng(11)
+    run_case(eng, lg, params, uniforms=rng.random(len(params)).astype(np.float32),
+             name="special")
+
+
+def test_denormal_probabilities(eng):
+    # probabilities in the subnormal range exercise the low end of the exact sums
+    V = 2000
+    x = np.linspace(-103.5, 0, V).astype(np.float32)
+    lg = np.stack([x, x[::-1].copy(), np.concatenate([x[:1000], np.full(1000, -90, np.float32)])])
+    params = [SP(temperature=1.0), SP(temperature=1.0, top_p=0.999), SP(temperature=0.5)]
+    run_case(eng, lg, params, uniforms=np.array([0.9999, 0.5, 0.999999], np.float32),
+             name="denormal")
+
+
+def test_draw_edges(eng):
+    # r = 0, r just below 1 (fall-through), r equal to a CDF value
+    V = 8
+    lg = np.tile(np.zeros(V, np.float32), (4, 1))
+    params = [SP(temperature=1.0)] * 4
+    us = np.array([0.0, 0.99999994, 0.125, 0.875], np.float32)
+    run_case(eng, lg, params, uniforms=us, name="draw_edges")
+
+
+# ---- streaming path: no top-k, windows over the probability order ---------
+
+@pytest.mark.parametrize("V,sd,p", [(50_000, 1.0, 0.99), (50_000, 0.05, 0.9), (20_000, 3.0, 0.5)])
+def test_large_path_topp_windows(eng, V, sd, p):
+    rng = np.random.default_rng(V + int(sd * 100))
+    B = 6
+    lg = rng.normal(0, sd, (B, V)).astype(np.float32)
+    params = [SP(temperature=1.0, top_p=p), SP(temperature=0.7, top_p=p),
+              SP(temperature=1.0, top_p=p, min_p=0.05), SP(temperature=1.3),
+              SP(temperature=1.0, top_p=p, repetition_penalty=1.3),
+              SP(temperature=1.0, top_k=V // 2, top_p=p)]
+    hists = [rng.integers(0, V, 100).astype(np.uint32) for _ in range(B)]
+    run_case(eng, lg, params, hists, rng.random(B).astype(np.float32), name=f"win{V}_{sd}_{p}",
+             check_pen=True)
+
+
+def test_unaligned_and_strided_rows(eng):
+    rng = np.random.default_rng(99)
+    V = 10_001
+    B = 5
+    lg = rng.normal(0, 2, (B, V)).astype(np.float32)
+    params = [SP(temperature=0.0), SP(temperature=1.0, top_k=30), SP(temperature=1.0, top_p=0.8),
+              SP(temperature=0.9), SP(temperature=1.0, top_k=3, top_p=0.5)]
+    run_case(eng, lg, params, uniforms=rng.random(B).astype(np.float32), name="stride",
+             row_stride=V + 3)
+
+
+def test_bf16_rows(eng):
+    from lumen_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(5)
+    V, B = 30_000, 8
+    bits = to_bf16_bits(rng.normal(0, 1, (B, V)).astype(np.float32))
+    f32 = (bits.astype(np.uint32) << 16).view(np.float32)
+    params = [SP(temperature=1.0, top_p=0.99)] * 4 + [SP(temperature=0.0), SP(temperature=1.0, top_k=20),
+                                                     SP(temperature=0.8), SP(temperature=1.0, top_p=0.5)]
+    log("case bf16")
+    rep = parity.compare(eng, f32, params, [np.zeros(0, np.uint32)] * B,
+                         rng.random(B).astype(np.float32), dtype="bf16", bf16_bits=bits)
+    assert_clean(rep, "bf16")
+
+
+def test_run_to_run_bit_identity(eng):
+    import torch
+
+    from lumen_amd.workloads import config3
+
+    w = config3(seed=31, V=40_000, B=16)
+    dev = torch.from_numpy(w.logits).cuda()
+    u = np.random.default_rng(1).random(16).astype(np.float32)
+    outs = []
+    for _ in range(3):
+        tr = torch.zeros((16, 16), dtype=torch.int32, device="cuda")
+        t, h = eng.sample_batch(dev, w.params, histories=w.histories, uniforms=u, trace=tr)
+        outs.append((h, tr.cpu().numpy().tobytes()))
+    assert outs[0] == outs[1] == outs[2]
