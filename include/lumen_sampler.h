@@ -103,6 +103,11 @@ typedef struct {
  * the library instead draws Xorshift64::next_f32 from rng_states[b]
  * (advancing it in place) for every row with temperature > 0, matching
  * `sample_logits(.., rng)` (sampling.rs:1004). Greedy rows consume no draw.
+ * uniforms_dev keeps the draws in device memory (no staging copy).
+ *
+ * Staging: per-row parameters and host-built penalty counts are copied to
+ * the device only when they differ from the previous call on the context;
+ * up to 8 rows travel inside the kernel arguments.
  */
 typedef struct {
     const void *logits;                 /* device */
@@ -125,6 +130,8 @@ typedef struct {
     const uint32_t *pen_counts;         /* device */
     const float *uniforms;              /* host, [batch]; may be NULL if rng_states */
     uint64_t *rng_states;               /* host, [batch] in/out; may be NULL */
+    const float *uniforms_dev;          /* device, [batch]; when non-NULL it is used
+                                           instead of uniforms / rng_states */
     uint32_t *tokens;                   /* device, [batch] output */
     lumen_row_trace *trace;             /* device, [batch] or NULL */
     float *penalized_out;               /* device, [batch][vocab] or NULL (debug) */

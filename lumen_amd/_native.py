@@ -90,6 +90,7 @@ class BatchC(ctypes.Structure):
         ("pen_counts", ctypes.c_void_p),
         ("uniforms", ctypes.POINTER(ctypes.c_float)),
         ("rng_states", ctypes.POINTER(ctypes.c_uint64)),
+        ("uniforms_dev", ctypes.c_void_p),
         ("tokens", ctypes.c_void_p),
         ("trace", ctypes.c_void_p),
         ("penalized_out", ctypes.c_void_p),

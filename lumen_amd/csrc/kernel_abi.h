@@ -56,6 +56,26 @@ enum RowStatus : uint32_t {
 };
 
 constexpr int kInlineRows = 8;
+constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
+constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
+
+// Per-row coordination block in device memory. Zero at allocation; the last
+// workgroup of a row to finish restores the counters to zero, so every
+// launch starts from a clean block.
+struct RowWs {
+  uint32_t arrive;       // last-arriver counter
+  uint32_t bar;          // spin barrier counter
+  uint32_t exit_;        // exit counter (resets the block)
+  uint32_t cand_n;       // candidates appended
+  uint32_t status;       // row failure bits
+  uint32_t pad[3];
+  uint32_t chain_flag[kMaxSlices];
+  float chain_c[kMaxSlices];
+  float part_max[kMaxSlices];
+  uint32_t part_nan[kMaxSlices];
+  uint64_t part_arg[kMaxSlices];
+  double part_e[kMaxSlices];
+};
 
 struct KernelArgs {
   const void* logits;        // [B][row_stride] f32 or bf16, device
@@ -76,8 +96,12 @@ struct KernelArgs {
   float* pen_out;            // optional [B][vocab] copy of penalized logits
   // Small batches pass their parameters and draws inside the kernel
   // arguments (no staging copy): used when inline_rows > 0.
-  uint32_t inline_rows;
-  uint32_t pad1;
+  RowWs* ws;                 // [B] coordination blocks
+  uint64_t* cand;            // [B][kCandCap] candidate buffers
+  uint32_t slices;           // workgroups per row (G)
+  uint32_t xcd_rows;         // 1: place all slices of a row on one XCD
+  uint32_t inline_rows;      // > 0: params come from inline_params
+  uint32_t inline_draws;     // != 0: draws come from inline_uniforms
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };

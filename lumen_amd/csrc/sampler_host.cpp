@@ -49,10 +49,15 @@ struct lumen_sampler {
   size_t pin_cap = 0;
   DevBuf stage;
   DevBuf pen_scratch;
+  DevBuf ws;    // [B] RowWs, zeroed at allocation, self-resetting afterwards
+  DevBuf cand;  // [B][kCandCap] candidate buffers
+  int cu_count = 0;
+  int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
   hipEvent_t staged = nullptr;  // recorded after the last staging copy
   bool staged_pending = false;
   std::vector<uint32_t> ids, cnts, offs;
   std::vector<uint32_t> tmp;
+  std::vector<char> img, last_img;  // static staging block: current / on the device
 };
 
 namespace {
@@ -222,6 +227,15 @@ int lumen_sampler_create(lumen_sampler** out, int device) {
     delete s;
     return LUMEN_ERR_CODE_OBJECT;
   }
+  if (hipDeviceGetAttribute(&s->cu_count, hipDeviceAttributeMultiprocessorCount, device) !=
+      hipSuccess)
+    s->cu_count = 0;
+  {
+    int per_cu = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, s->fn, 1024, 0) != hipSuccess)
+      per_cu = 0;
+    s->max_resident = per_cu * s->cu_count;
+  }
   if (hipEventCreateWithFlags(&s->staged, hipEventDisableTiming) != hipSuccess) {
     (void)hipModuleUnload(s->module);
     delete s;
@@ -238,6 +252,8 @@ void lumen_sampler_destroy(lumen_sampler* s) {
   if (s->pin) (void)hipHostFree(s->pin);
   if (s->stage.p) (void)hipFree(s->stage.p);
   if (s->pen_scratch.p) (void)hipFree(s->pen_scratch.p);
+  if (s->ws.p) (void)hipFree(s->ws.p);
+  if (s->cand.p) (void)hipFree(s->cand.p);
   if (s->staged) (void)hipEventDestroy(s->staged);
   if (s->module) (void)hipModuleUnload(s->module);
   delete s;
@@ -252,7 +268,7 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
     return fail(LUMEN_ERR_INVALID, "dtype must be LUMEN_DTYPE_F32 or LUMEN_DTYPE_BF16");
   if (V > 0 && (!bt->logits || bt->row_stride < V))
     return fail(LUMEN_ERR_INVALID, "logits missing or row_stride < vocab");
-  if (!bt->uniforms && !bt->rng_states) {
+  if (!bt->uniforms && !bt->rng_states && !bt->uniforms_dev) {
     for (uint32_t b = 0; b < B; ++b)
       if (bt->params[b].temperature > 0.0f)
         return fail(LUMEN_ERR_INVALID, "sampled rows need uniforms or rng_states");
@@ -289,7 +305,7 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
       count_window(s, bt->history + h0, h1 - h0, p.repeat_last_n);
     s->offs[b + 1] = (uint32_t)s->ids.size();
     any_pen |= (rows[b].flags & lumen::kPen) != 0;
-    if (V > 0 && !(rows[b].flags & lumen::kGreedy)) {
+    if (V > 0 && !bt->uniforms_dev && !(rows[b].flags & lumen::kGreedy)) {
       // exactly one draw per sampled row (sampling.rs:1004)
       draws[b] = bt->rng_states ? lumen_xorshift64_next_f32(&bt->rng_states[b]) : bt->uniforms[b];
     }
@@ -329,58 +345,78 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
   ka.trace = reinterpret_cast<lumen::RowTrace*>(bt->trace);
   ka.pen_out = bt->penalized_out;
 
-  // staging layout: [params][uniforms][offs][ids][cnts]
+  // Staging. Two blocks share one pinned host buffer and one device buffer:
+  //   static block [params][offs][ids][cnts]: copied only when its bytes
+  //                differ from what the device buffer already holds;
+  //   draw block   [uniforms]: copied every call unless the draws are inline
+  //                kernel arguments or already in device memory.
   const bool inl = B <= (uint32_t)lumen::kInlineRows;
   const bool host_csr = !bt->pen_offsets;
-  size_t off_params = 0;
-  size_t off_unif = off_params + (inl ? 0 : sizeof(RowParams) * B);
-  size_t off_offs = (off_unif + (inl ? 0 : sizeof(float) * B) + 15) & ~size_t(15);
-  size_t off_ids = off_offs + (host_csr ? sizeof(uint32_t) * (B + 1) : 0);
-  size_t off_cnts = off_ids + (host_csr ? sizeof(uint32_t) * s->ids.size() : 0);
-  size_t total = off_cnts + (host_csr ? sizeof(uint32_t) * s->cnts.size() : 0);
+  auto a16 = [](size_t x) { return (x + 15) & ~size_t(15); };
+  const size_t off_offs = inl ? 0 : a16(sizeof(RowParams) * B);
+  const size_t off_ids = off_offs + (host_csr ? sizeof(uint32_t) * (B + 1) : 0);
+  const size_t off_cnts = off_ids + (host_csr ? sizeof(uint32_t) * s->ids.size() : 0);
+  const size_t static_sz = a16(off_cnts + (host_csr ? sizeof(uint32_t) * s->cnts.size() : 0));
+  const bool draw_block = !bt->uniforms_dev && !inl;
+  const size_t total = static_sz + (draw_block ? sizeof(float) * B : 0);
   if (inl) {
     ka.inline_rows = B;
-    for (uint32_t b = 0; b < B; ++b) {
-      ka.inline_params[b] = rows[b];
-      ka.inline_uniforms[b] = draws[b];
-    }
+    for (uint32_t b = 0; b < B; ++b) ka.inline_params[b] = rows[b];
+  }
+  if (bt->uniforms_dev) {
+    ka.uniforms = bt->uniforms_dev;
+  } else if (inl) {
+    ka.inline_draws = 1;
+    for (uint32_t b = 0; b < B; ++b) ka.inline_uniforms[b] = draws[b];
   }
   if (total > 0) {
-    if (s->staged_pending) {
-      if (hipEventSynchronize(s->staged) != hipSuccess) return LUMEN_ERR_HIP;
-      s->staged_pending = false;
+    s->img.assign(static_sz, 0);
+    if (!inl) std::memcpy(s->img.data(), rows.data(), sizeof(RowParams) * B);
+    if (host_csr) {
+      std::memcpy(s->img.data() + off_offs, s->offs.data(), sizeof(uint32_t) * (B + 1));
+      if (!s->ids.empty()) {
+        std::memcpy(s->img.data() + off_ids, s->ids.data(), sizeof(uint32_t) * s->ids.size());
+        std::memcpy(s->img.data() + off_cnts, s->cnts.data(), sizeof(uint32_t) * s->cnts.size());
+      }
     }
-    if (s->pin_cap < total) {
-      if (s->pin) (void)hipHostFree(s->pin);
-      s->pin = nullptr;
-      s->pin_cap = 0;
-      size_t cap = std::max<size_t>(total, 65536);
-      if (hipHostMalloc(&s->pin, cap, hipHostMallocDefault) != hipSuccess) return LUMEN_ERR_HIP;
-      s->pin_cap = cap;
-    }
+    const size_t dev_cap_before = s->stage.cap;
     int rc = ensure_dev(s->stage, total);
     if (rc != LUMEN_OK) return rc;
-    char* hp = static_cast<char*>(s->pin);
-    char* dp = static_cast<char*>(s->stage.p);
-    if (!inl) {
-      std::memcpy(hp + off_params, rows.data(), sizeof(RowParams) * B);
-      std::memcpy(hp + off_unif, draws.data(), sizeof(float) * B);
-      ka.params = reinterpret_cast<const RowParams*>(dp + off_params);
-      ka.uniforms = reinterpret_cast<const float*>(dp + off_unif);
-    }
-    if (host_csr) {
-      std::memcpy(hp + off_offs, s->offs.data(), sizeof(uint32_t) * (B + 1));
-      if (!s->ids.empty()) {
-        std::memcpy(hp + off_ids, s->ids.data(), sizeof(uint32_t) * s->ids.size());
-        std::memcpy(hp + off_cnts, s->cnts.data(), sizeof(uint32_t) * s->cnts.size());
+    if (s->stage.cap != dev_cap_before) s->last_img.clear();  // new device buffer
+    const bool copy_static = static_sz > 0 && s->img != s->last_img;
+    if (copy_static || draw_block) {
+      if (s->staged_pending) {
+        if (hipEventSynchronize(s->staged) != hipSuccess) return fail(LUMEN_ERR_HIP, "staging wait");
+        s->staged_pending = false;
       }
+      if (s->pin_cap < total) {
+        if (s->pin) (void)hipHostFree(s->pin);
+        s->pin = nullptr;
+        s->pin_cap = 0;
+        size_t cap = std::max<size_t>(total, 65536);
+        if (hipHostMalloc(&s->pin, cap, hipHostMallocDefault) != hipSuccess)
+          return fail(LUMEN_ERR_HIP, "pinned staging allocation");
+        s->pin_cap = cap;
+      }
+      char* hp = static_cast<char*>(s->pin);
+      char* dp = static_cast<char*>(s->stage.p);
+      size_t lo = copy_static ? 0 : static_sz;
+      if (copy_static) std::memcpy(hp, s->img.data(), static_sz);
+      if (draw_block) std::memcpy(hp + static_sz, draws.data(), sizeof(float) * B);
+      if (hipMemcpyAsync(dp + lo, hp + lo, total - lo, hipMemcpyHostToDevice, st) != hipSuccess)
+        return fail(LUMEN_ERR_HIP, "staging copy");
+      if (hipEventRecord(s->staged, st) != hipSuccess) return fail(LUMEN_ERR_HIP, "event record");
+      s->staged_pending = true;
+      if (copy_static) s->last_img = s->img;
+    }
+    char* dp = static_cast<char*>(s->stage.p);
+    if (!inl) ka.params = reinterpret_cast<const RowParams*>(dp);
+    if (draw_block) ka.uniforms = reinterpret_cast<const float*>(dp + static_sz);
+    if (host_csr) {
       ka.hist_off = reinterpret_cast<const uint32_t*>(dp + off_offs);
       ka.hist_ids = reinterpret_cast<const uint32_t*>(dp + off_ids);
       ka.hist_cnt = reinterpret_cast<const uint32_t*>(dp + off_cnts);
     }
-    if (hipMemcpyAsync(dp, hp, total, hipMemcpyHostToDevice, st) != hipSuccess) return LUMEN_ERR_HIP;
-    if (hipEventRecord(s->staged, st) != hipSuccess) return LUMEN_ERR_HIP;
-    s->staged_pending = true;
   }
   if (!host_csr) {
     ka.hist_off = bt->pen_offsets;
@@ -394,10 +430,36 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
     ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
     ka.pen_stride = stride;
   }
+  // Workgroups per row: enough to occupy every CU once (all co-resident),
+  // at most kMaxSlices. With 8+ rows, a row's slices share one XCD.
+  uint32_t G = 1;
+  const uint32_t padded = B >= 8 ? ((B + 7u) / 8u) * 8u : B;
+  if (s->max_resident > 0 && std::getenv("LUMEN_SAMPLER_SINGLE") == nullptr)
+    G = std::max<uint32_t>(1u, std::min<uint32_t>(lumen::kMaxSlices,
+                                                  (uint32_t)s->max_resident / padded));
+  ka.slices = G;
+  ka.xcd_rows = (B >= 8 && G > 1) ? 1u : 0u;
+  const uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
+  if (G > 1) {
+    const size_t ws_bytes = sizeof(lumen::RowWs) * B;
+    if (s->ws.cap < ws_bytes) {
+      int rc = ensure_dev(s->ws, ws_bytes);
+      if (rc != LUMEN_OK) return rc;
+      // zero once at allocation; afterwards each launch leaves it zeroed
+      if (hipMemset(s->ws.p, 0, s->ws.cap) != hipSuccess) return fail(LUMEN_ERR_HIP, "workspace init");
+    }
+    int rc = ensure_dev(s->cand, sizeof(uint64_t) * lumen::kCandCap * B);
+    if (rc != LUMEN_OK) return rc;
+    ka.ws = static_cast<lumen::RowWs*>(s->ws.p);
+    ka.cand = static_cast<uint64_t*>(s->cand.p);
+    void* params[] = {&ka};
+    hipError_t e = hipModuleLaunchCooperativeKernel(s->fn, nblocks, 1, 1, 1024, 1, 1, 0, st, params);
+    return hip_fail(e);
+  }
   size_t argsz = sizeof(ka);
   void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &argsz,
                  HIP_LAUNCH_PARAM_END};
-  hipError_t e = hipModuleLaunchKernel(s->fn, B, 1, 1, 1024, 1, 1, 0, st, nullptr, cfg);
+  hipError_t e = hipModuleLaunchKernel(s->fn, nblocks, 1, 1, 1024, 1, 1, 0, st, nullptr, cfg);
   return hip_fail(e);
 }
 

@@ -124,6 +124,27 @@ __device__ __forceinline__ void row_foreach(const Row& r, F&& f) {
   }
 }
 
+// f(i, v) for every element of [lo, hi).
+template <class F>
+__device__ __forceinline__ void range_foreach(const Row& r, uint32_t lo, uint32_t hi, F&& f) {
+  if (lo >= hi) return;
+  for (uint32_t g0 = lo / 4u + threadIdx.x; g0 * 4u < hi; g0 += 4u * kThreads) {
+    float v[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t i = (g0 + u * kThreads) * 4u;
+      if (i < hi) r.load4(i, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t i = (g0 + u * kThreads) * 4u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (i + j >= lo && i + j < hi) f(i + j, v[u][j]);
+    }
+  }
+}
+
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -376,6 +397,27 @@ struct Final {  // what the final stage needs to know about the list
   uint32_t n;
 };
 
+__device__ __forceinline__ void init_trace(RowTrace& tr, uint32_t V) {
+  tr.status = 0; tr.path = 0; tr.topk_cutoff_key = 0; tr.topk_survivors = V; tr.topp_sum = 0.f;
+  tr.topp_kept = 0; tr.topp_cum = 0.f; tr.windows = 0; tr.final_max = 0.f; tr.final_sum = 0.f;
+  tr.cdf_before = 0.f; tr.cdf_at = 0.f; tr.token = 0; tr.passes = 0; tr.pad[0] = tr.pad[1] = 0;
+}
+
+__device__ __forceinline__ Row make_row(const KernelArgs& a, int b) {
+  Row row;
+  if (a.dtype == 0) {
+    row.f = reinterpret_cast<const float*>(a.logits) + (uint64_t)b * a.row_stride;
+    row.h = nullptr;
+    row.vec = ((reinterpret_cast<uintptr_t>(row.f) & 15u) == 0);
+  } else {
+    row.f = nullptr;
+    row.h = reinterpret_cast<const uint16_t*>(a.logits) + (uint64_t)b * a.row_stride;
+    row.vec = ((reinterpret_cast<uintptr_t>(row.h) & 7u) == 0);
+  }
+  row.V = a.vocab;
+  return row;
+}
+
 __device__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrace& tr) {
   if (threadIdx.x == 0) {
     a.tokens[b] = token;
@@ -451,28 +493,116 @@ __device__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint3
   return V - 1;
 }
 
-extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs a) {
-  __shared__ Smem s;
-  const int b = blockIdx.x;
+// Everything after top-k for a row whose survivors are in s.A as
+// (idx << 32) | key, ascending idx (sampling.rs:502-526): top-p on the list
+// (unless already applied), min-p, temperature, softmax, draw.
+__device__ void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
+                           bool topp_done, float rdraw, Smem& s, RowTrace& tr) {
+  const int t = threadIdx.x;
+  const uint32_t V = a.vocab;
+  tr.path |= 2u;
+  // top-p on the list (sampling.rs:942-967)
+  bool lpred = false;  // list-level top-p predicate active
+  bool lunif = false;
+  uint32_t lplim = 0;
+  float lpstar = 0.f, lm1 = 0.f, lS1 = 1.f;
+  uint32_t ljstar = 0;
+  const uint32_t n = nlist;
+  auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
+  if ((P.flags & kTopP) && !topp_done) {
+    float m = kNegInf;
+    uint32_t nan = 0;
+    for (uint32_t j = t; j < n; j += kThreads) {
+      m = rmax(m, lv(j));
+      nan |= is_nan(lv(j)) ? 1u : 0u;
+    }
+    m = block_rmax(m, s);
+    nan = block_or_u32(nan, s);
+    lm1 = m;
+    if (!is_finite(m)) {
+      tr.path |= 8u;
+      float u = __fdiv_rn(1.0f, __uint2float_rn(V));
+      EcssResult e = const_ecss(V, u, kEcssFindGe, P.top_p, s);
+      if (e.found) {
+        lunif = true;
+        lplim = (uint32_t)e.pos;
+        tr.topp_kept = lplim + 1;
+      } else {
+        tr.topp_kept = V;
+      }
+      tr.topp_cum = e.c;
+    } else if (nan) {
+      tr.topp_sum = __uint_as_float(0x7fc00000u);
+      tr.topp_kept = V;
+    } else {
+      EcssResult e = list_ecss(
+          n, [&](uint32_t j) { return expf_glibc(__fsub_rn(lv(j), lm1)); }, kEcssSum, 0.f, 0.f, s);
+      lS1 = e.c;
+      tr.topp_sum = lS1;
+      for (uint32_t j = t; j < n; j += kThreads) {
+        float p = __fdiv_rn(expf_glibc(__fsub_rn(lv(j), lm1)), lS1);
+        s.Bk[j] = ((uint64_t)(~__float_as_uint(p)) << 32) | j;
+      }
+      __syncthreads();
+      sort_u64_asc(s.Bk, n);
+      EcssResult w = list_ecss(
+          n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); },
+          kEcssFindGe, P.top_p, 0.f, s);
+      if (w.found) {
+        lpred = true;
+        lpstar = __uint_as_float(~(uint32_t)(s.Bk[w.pos] >> 32));
+        ljstar = (uint32_t)s.Bk[w.pos];
+        tr.topp_kept = (uint32_t)w.pos + 1u;
+      } else {
+        tr.topp_kept = V;
+      }
+      tr.topp_cum = w.c;
+    }
+  }
+  // compact the list to the entries that survive top-p
+  if (lpred || lunif) {
+    if (t == 0) s.cnt = 0;
+    __syncthreads();
+    // entries are kept in index order: process in order with a block scan
+    for (uint32_t base = 0; base < n; base += kThreads) {
+      const uint32_t j = base + t;
+      bool keep = false;
+      uint64_t e = 0;
+      if (j < n) {
+        e = s.A[j];
+        if (lunif) {
+          keep = (uint32_t)(e >> 32) <= lplim;
+        } else {
+          float p = __fdiv_rn(expf_glibc(__fsub_rn(lv(j), lm1)), lS1);
+          keep = p > lpstar || (p == lpstar && j <= ljstar);
+        }
+      }
+      uint32_t inc = block_incl_scan_u32(keep ? 1u : 0u, s);
+      const uint32_t c0 = s.cnt;
+      __syncthreads();
+      if (keep) s.Bk[c0 + inc - 1] = e;
+      if (t == kThreads - 1) s.cnt = c0 + inc;
+      __syncthreads();
+    }
+    const uint32_t nk = s.cnt;
+    for (uint32_t j = t; j < nk; j += kThreads) s.A[j] = s.Bk[j];
+    __syncthreads();
+    nlist = nk;
+  }
+  uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr);
+  write_result(a, b, tok, tr);
+}
+
+// The whole sampler for row b, run by one workgroup (used directly when a
+// row has one workgroup, and as the fallback of the split paths).
+__device__ void row_single(const KernelArgs& a, int b, Smem& s) {
   const int t = threadIdx.x;
   const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
   const uint32_t V = a.vocab;
   RowTrace tr;
-  tr.status = 0; tr.path = 0; tr.topk_cutoff_key = 0; tr.topk_survivors = V; tr.topp_sum = 0.f;
-  tr.topp_kept = 0; tr.topp_cum = 0.f; tr.windows = 0; tr.final_max = 0.f; tr.final_sum = 0.f;
-  tr.cdf_before = 0.f; tr.cdf_at = 0.f; tr.token = 0; tr.passes = 0; tr.pad[0] = tr.pad[1] = 0;
+  init_trace(tr, V);
 
-  Row row;
-  if (a.dtype == 0) {
-    row.f = reinterpret_cast<const float*>(a.logits) + (uint64_t)b * a.row_stride;
-    row.h = nullptr;
-    row.vec = ((reinterpret_cast<uintptr_t>(row.f) & 15u) == 0);
-  } else {
-    row.f = nullptr;
-    row.h = reinterpret_cast<const uint16_t*>(a.logits) + (uint64_t)b * a.row_stride;
-    row.vec = ((reinterpret_cast<uintptr_t>(row.h) & 7u) == 0);
-  }
-  row.V = V;
+  Row row = make_row(a, b);
 
   // ---- penalties: materialize the penalized row (sampling.rs:850-879) ----
   const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
@@ -509,7 +639,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
     return;
   }
 
-  const float rdraw = a.inline_rows ? a.inline_uniforms[b] : a.uniforms[b];
+  const float rdraw = a.inline_draws ? a.inline_uniforms[b] : a.uniforms[b];
   bool small = false;   // survivors in s.A as (idx << 32) | key, ascending idx
   uint32_t nlist = 0;
   bool topp_done = false;
@@ -781,97 +911,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
   }
 
   if (small) {
-    tr.path |= 2u;
-    // top-p on the list (sampling.rs:942-967)
-    bool lpred = false;  // list-level top-p predicate active
-    bool lunif = false;
-    uint32_t lplim = 0;
-    float lpstar = 0.f, lm1 = 0.f, lS1 = 1.f;
-    uint32_t ljstar = 0;
-    const uint32_t n = nlist;
-    auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
-    if ((P.flags & kTopP) && !topp_done) {
-      float m = kNegInf;
-      uint32_t nan = 0;
-      for (uint32_t j = t; j < n; j += kThreads) {
-        m = rmax(m, lv(j));
-        nan |= is_nan(lv(j)) ? 1u : 0u;
-      }
-      m = block_rmax(m, s);
-      nan = block_or_u32(nan, s);
-      lm1 = m;
-      if (!is_finite(m)) {
-        tr.path |= 8u;
-        float u = __fdiv_rn(1.0f, __uint2float_rn(V));
-        EcssResult e = const_ecss(V, u, kEcssFindGe, P.top_p, s);
-        if (e.found) {
-          lunif = true;
-          lplim = (uint32_t)e.pos;
-          tr.topp_kept = lplim + 1;
-        } else {
-          tr.topp_kept = V;
-        }
-        tr.topp_cum = e.c;
-      } else if (nan) {
-        tr.topp_sum = __uint_as_float(0x7fc00000u);
-        tr.topp_kept = V;
-      } else {
-        EcssResult e = list_ecss(
-            n, [&](uint32_t j) { return expf_glibc(__fsub_rn(lv(j), lm1)); }, kEcssSum, 0.f, 0.f, s);
-        lS1 = e.c;
-        tr.topp_sum = lS1;
-        for (uint32_t j = t; j < n; j += kThreads) {
-          float p = __fdiv_rn(expf_glibc(__fsub_rn(lv(j), lm1)), lS1);
-          s.Bk[j] = ((uint64_t)(~__float_as_uint(p)) << 32) | j;
-        }
-        __syncthreads();
-        sort_u64_asc(s.Bk, n);
-        EcssResult w = list_ecss(
-            n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); },
-            kEcssFindGe, P.top_p, 0.f, s);
-        if (w.found) {
-          lpred = true;
-          lpstar = __uint_as_float(~(uint32_t)(s.Bk[w.pos] >> 32));
-          ljstar = (uint32_t)s.Bk[w.pos];
-          tr.topp_kept = (uint32_t)w.pos + 1u;
-        } else {
-          tr.topp_kept = V;
-        }
-        tr.topp_cum = w.c;
-      }
-    }
-    // compact the list to the entries that survive top-p
-    if (lpred || lunif) {
-      if (t == 0) s.cnt = 0;
-      __syncthreads();
-      // entries are kept in index order: process in order with a block scan
-      for (uint32_t base = 0; base < n; base += kThreads) {
-        const uint32_t j = base + t;
-        bool keep = false;
-        uint64_t e = 0;
-        if (j < n) {
-          e = s.A[j];
-          if (lunif) {
-            keep = (uint32_t)(e >> 32) <= lplim;
-          } else {
-            float p = __fdiv_rn(expf_glibc(__fsub_rn(lv(j), lm1)), lS1);
-            keep = p > lpstar || (p == lpstar && j <= ljstar);
-          }
-        }
-        uint32_t inc = block_incl_scan_u32(keep ? 1u : 0u, s);
-        const uint32_t c0 = s.cnt;
-        __syncthreads();
-        if (keep) s.Bk[c0 + inc - 1] = e;
-        if (t == kThreads - 1) s.cnt = c0 + inc;
-        __syncthreads();
-      }
-      const uint32_t nk = s.cnt;
-      for (uint32_t j = t; j < nk; j += kThreads) s.A[j] = s.Bk[j];
-      __syncthreads();
-      nlist = nk;
-    }
-    uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr);
-    write_result(a, b, tok, tr);
+    small_path(a, b, P, nlist, topp_done, rdraw, s, tr);
     return;
   }
 
@@ -946,4 +986,581 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
   write_result(a, b, tok, tr);
 }
 
+
+// ------------------------------------------------------------ row groups
+//
+// With G > 1 workgroups per row, workgroup `sl` owns the slice
+// [sl*per, (sl+1)*per) of its row (per a multiple of 16). The row's workgroups
+// coordinate through a RowWs block in device memory:
+//  * greedy and top-k rows use a last-arriver pattern (no waiting);
+//  * top-p rows use one row barrier and a chain in which slice sl waits for
+//    the exact running sum of slice sl-1. Every wait is bounded; on timeout
+//    the row reports a failure instead of waiting further.
+// All workgroups of a launch are co-resident (cooperative launch).
+
+constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr uint32_t kSampleN = 4096;
+
+struct Slice {
+  uint32_t lo, hi;
+};
+
+__device__ __forceinline__ Slice slice_bounds(uint32_t V, uint32_t G, uint32_t sl) {
+  uint32_t per = ((V + G - 1u) / G + 15u) & ~15u;
+  uint32_t lo = min(V, sl * per), hi = min(V, lo + per);
+  return Slice{lo, hi};
+}
+
+// Makes this workgroup's global writes visible at device scope and arrives on
+// *ctr; returns the previous count (uniform across the workgroup).
+__device__ uint32_t wg_arrive(uint32_t* ctr, Smem& s) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s.misc_u[2] = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const uint32_t old = s.misc_u[2];
+  __threadfence();
+  __syncthreads();
+  return old;
+}
+
+// Waits until *ctr >= target (acquire). Returns false on timeout.
+__device__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem& s) {
+  if (threadIdx.x == 0) {
+    uint32_t n = 0, ok = 1;
+    while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++n > kSpinLimit) {
+        ok = 0;
+        break;
+      }
+    }
+    s.misc_u[3] = ok;
+  }
+  __syncthreads();
+  const bool ok = s.misc_u[3] != 0;
+  __threadfence();
+  __syncthreads();
+  return ok;
+}
+
+// Wave-aggregated append of `val` to a row's global candidate buffer.
+__device__ __forceinline__ void cand_push(uint64_t* cand, uint32_t* cnt, bool p, uint64_t val) {
+  unsigned long long m = __ballot(p);
+  if (!m) return;
+  const int lane = threadIdx.x & 63;
+  const int leader = __ffsll((long long)m) - 1;
+  uint32_t base = 0;
+  if (lane == leader)
+    base = __hip_atomic_fetch_add(cnt, (uint32_t)__popcll(m), __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  base = __shfl(base, leader, 64);
+  if (p) {
+    uint32_t off = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+    if (off < (uint32_t)kCandCap) cand[off] = val;
+  }
+}
+
+// Key threshold such that about `target` keys of the row are >= it,
+// estimated from a fixed strided sample, so every workgroup of the row
+// computes the same value. 0 selects everything.
+__device__ uint32_t sample_threshold(const Row& row, uint32_t V, uint32_t target, Smem& s) {
+  if (V <= kSampleN || target >= V) return 0u;
+  const uint32_t r = (uint32_t)(((uint64_t)target * kSampleN + V - 1) / V);
+  if (r == 0u || r > kSampleN) return 0u;
+  for (uint32_t j = threadIdx.x; j < kSampleN; j += kThreads) {
+    uint32_t i = (uint32_t)(((uint64_t)j * V) / kSampleN);
+    s.A[j] = (uint64_t)(~tkey(row.at(i))) << 32;
+  }
+  __syncthreads();
+  sort_u64_asc(s.A, kSampleN);
+  const uint32_t tau = ~(uint32_t)(s.A[r - 1] >> 32);
+  __syncthreads();
+  return tau;
+}
+
+// LDS bitmap of the history ids that fall in [lo, hi) (bit i - lo), kept in
+// the Bk area, which is free during slice passes.
+__device__ uint32_t* slice_bitmap(const KernelArgs& a, int b, Slice sc, Smem& s) {
+  uint32_t* bm = reinterpret_cast<uint32_t*>(s.Bk);
+  const uint32_t nw = (sc.hi - sc.lo + 31u) / 32u;
+  for (uint32_t i = threadIdx.x; i < nw; i += kThreads) bm[i] = 0u;
+  __syncthreads();
+  const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+  for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
+    uint32_t id = a.hist_ids[j];
+    if (id >= sc.lo && id < sc.hi) atomicOr(&bm[(id - sc.lo) >> 5], 1u << ((id - sc.lo) & 31u));
+  }
+  __syncthreads();
+  return bm;
+}
+
+__device__ __forceinline__ bool bm_test(const uint32_t* bm, uint32_t off) {
+  return (bm[off >> 5] >> (off & 31u)) & 1u;
+}
+
+// Debug copy of the penalized logits of the slice.
+__device__ void slice_pen_out(const KernelArgs& a, int b, const Row& row, Slice sc,
+                              const RowParams& P, bool pen) {
+  float* po = a.pen_out + (uint64_t)b * a.vocab;
+  range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) { po[i] = v; });
+  __threadfence();
+  __syncthreads();
+  if (pen) {
+    const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+    for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
+      uint32_t id = a.hist_ids[j];
+      if (id >= sc.lo && id < sc.hi) po[id] = penalize(row.at(id), a.hist_cnt[j], P);
+    }
+  }
+}
+
+// Greedy: per-slice argmax, the last workgroup to arrive combines.
+__device__ void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                             const RowParams& P, const Row& row, RowWs& ws, Smem& s) {
+  const uint32_t V = a.vocab;
+  const Slice sc = slice_bounds(V, G, sl);
+  const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
+  if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
+  const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
+  uint64_t best = 0;
+  range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
+    if (pen && bm_test(bm, i - sc.lo)) return;
+    uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+    best = k > best ? k : best;
+  });
+  if (pen) {
+    const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+    for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
+      uint32_t id = a.hist_ids[j];
+      if (id >= sc.lo && id < sc.hi) {
+        uint64_t k = ((uint64_t)tkey(penalize(row.at(id), a.hist_cnt[j], P)) << 32) |
+                     (uint64_t)(0xffffffffu - id);
+        best = k > best ? k : best;
+      }
+    }
+  }
+  best = block_max_u64(best, s);
+  if (threadIdx.x == 0) ws.part_arg[sl] = best;
+  const uint32_t old = wg_arrive(&ws.arrive, s);
+  if (old != G - 1u) return;
+  uint64_t m = 0;
+  for (uint32_t i = 0; i < G; ++i) {
+    uint64_t u = __hip_atomic_load(&ws.part_arg[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    m = u > m ? u : m;
+  }
+  RowTrace tr;
+  init_trace(tr, V);
+  tr.path = 1u;
+  tr.passes = 1;
+  write_result(a, b, 0xffffffffu - (uint32_t)m, tr);
+}
+
+// Top-k: a sampled threshold, one compaction pass per slice into the row's
+// candidate buffer, and the last workgroup finishes on the LDS list. If the
+// sample missed (fewer than k or more than the buffer holds), the finisher
+// runs the exact single-workgroup path.
+__device__ void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                           const RowParams& P, const Row& row, RowWs& ws, uint64_t* cand,
+                           float rdraw, Smem& s) {
+  const uint32_t V = a.vocab;
+  const uint32_t k = P.top_k;
+  const Slice sc = slice_bounds(V, G, sl);
+  const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
+  if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
+  const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
+  const uint32_t tau = sample_threshold(row, V, target, s);
+  const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
+  range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
+    const uint32_t kk = tkey(v);
+    const bool in = kk >= tau && !(pen && bm_test(bm, i - sc.lo));
+    cand_push(cand, &ws.cand_n, in, ((uint64_t)(~kk) << 32) | i);
+  });
+  if (pen) {
+    const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+    for (uint32_t base = h0; base < h1; base += kThreads) {
+      const uint32_t j = base + threadIdx.x;
+      bool in = false;
+      uint32_t kk = 0, id = 0;
+      if (j < h1) {
+        id = a.hist_ids[j];
+        if (id >= sc.lo && id < sc.hi) {
+          kk = tkey(penalize(row.at(id), a.hist_cnt[j], P));
+          in = kk >= tau;
+        }
+      }
+      cand_push(cand, &ws.cand_n, in, ((uint64_t)(~kk) << 32) | id);
+    }
+  }
+  const uint32_t old = wg_arrive(&ws.arrive, s);
+  if (old != G - 1u) return;
+  const uint32_t n = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (n < k || n > (uint32_t)kCandCap) {
+    row_single(a, b, s);
+    return;
+  }
+  RowTrace tr;
+  init_trace(tr, V);
+  tr.passes = 1;
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) s.A[j] = cand[j];
+  __syncthreads();
+  sort_u64_asc(s.A, n);  // descending key, then ascending index
+  uint32_t ns;
+  uint32_t cut;
+  if (k == 1) {
+    // sampling.rs:913-921: exactly the lowest-index maximum
+    ns = 1;
+    cut = ~(uint32_t)(s.A[0] >> 32);
+  } else {
+    cut = ~(uint32_t)(s.A[k - 1] >> 32);
+    uint32_t c = 0;
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) c += (~(uint32_t)(s.A[j] >> 32) >= cut) ? 1u : 0u;
+    ns = block_sum_u32(c, s);
+  }
+  for (uint32_t j = threadIdx.x; j < ns; j += kThreads) {
+    uint64_t e = s.A[j];
+    s.A[j] = ((uint64_t)(uint32_t)e << 32) | (uint64_t)(~(uint32_t)(e >> 32));
+  }
+  __syncthreads();
+  sort_u64_asc(s.A, ns);  // ascending index
+  tr.topk_cutoff_key = cut;
+  tr.topk_survivors = ns;
+  small_path(a, b, P, ns, false, rdraw, s, tr);
+}
+
+__device__ double block_excl_scan_f64(double v, Smem& s, double* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  double inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    double o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  __shared__ double wt[kWaves];
+  if (lane == 63) wt[w] = inc;
+  __syncthreads();
+  double pre = 0.0, tot = 0.0;
+  for (int i = 0; i < kWaves; ++i) {
+    if (i < w) pre += wt[i];
+    tot += wt[i];
+  }
+  __syncthreads();
+  *total = tot;
+  return pre + inc - v;
+}
+
+// Lower bound of the binade holding a non-negative value, as f32 bits.
+__device__ __forceinline__ uint32_t binade_bits(double x) {
+  float f = __double2float_rz(x > 0.0 ? x : 0.0);
+  return __float_as_uint(f) & 0xff800000u;
+}
+
+// Exact sequential f32 sum of expf(v - m1) over slice [lo, hi), continuing
+// the running sum of the slices before it. The slice is cut into sub-chunks
+// of kThreads * M elements; in each, thread t owns M consecutive elements.
+// Before waiting for the previous slice, every thread computes its
+// summands, a f64 estimate of the running sum at its start, and the parity
+// maps for the one or two binades that sum can be in; the maps are parked in
+// LDS (the list area is idle in this phase). After the wait only block scans
+// remain, plus an exact replay (summands recomputed) of each thread in which
+// the running sum changes binade. Publishes the outgoing sum in
+// ws.chain_c[sl].
+struct ChainMaps {
+  uint32_t ba, bb;  // binade bases (f32 bits) the maps were built for
+  PMap ma, mb;
+};
+
+template <int M>
+__device__ __forceinline__ void chain_load(const Row& row, Slice sc, uint32_t i0, float m1,
+                                           float (&x)[M]) {
+#pragma unroll
+  for (int q = 0; q < M / 4; ++q) {
+    float v[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
+    const uint32_t i = i0 + 4u * q;
+    if (i < sc.hi) row.load4(i, v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < sc.hi) ? v[j] : kNegInf;
+  }
+}
+
+template <int M>
+__device__ float slice_chain_sum(const Row& row, Slice sc, float m1, double p_slice, RowWs& ws,
+                                 uint32_t sl, Smem& s, bool* ok) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint32_t chunk = (uint32_t)kThreads * M;
+  const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;  // <= 4 (LDS map budget)
+  ChainMaps* maps = reinterpret_cast<ChainMaps*>(s.A);
+  double pre = p_slice;
+  for (uint32_t q = 0; q < nq; ++q) {
+    const uint32_t i0 = sc.lo + q * chunk + (uint32_t)t * M;
+    float x[M];
+    chain_load<M>(row, sc, i0, m1, x);
+    double d = 0.0;
+#pragma unroll
+    for (int j = 0; j < M; ++j) d += (double)__expf(x[j] - m1);
+    double tot;
+    const double pt = pre + block_excl_scan_f64(d, s, &tot);
+    pre += tot;
+#pragma unroll
+    for (int j = 0; j < M; ++j) x[j] = expf_glibc(__fsub_rn(x[j], m1));
+    // |C - P| <= (elements before) * 2^-24 * C for a sequential f32 sum of
+    // non-negative terms; 1e-5 covers the estimate's own error
+    const double eps = (double)i0 * 0x1.0p-24 * 1.01 + 1e-5;
+    ChainMaps cm;
+    cm.ba = binade_bits(pt * (1.0 - eps));
+    cm.bb = binade_bits(pt * (1.0 + eps));
+    {
+      float y0 = __uint_as_float(cm.ba), y1 = __uint_as_float(cm.ba | 1u);
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        y0 = __fadd_rn(y0, x[j]);
+        y1 = __fadd_rn(y1, x[j]);
+      }
+      uint32_t n0 = __float_as_uint(y0) - cm.ba, n1 = __float_as_uint(y1) - (cm.ba | 1u);
+      cm.ma.a0 = n0 > kSat ? kSat : n0;
+      cm.ma.a1 = n1 > kSat ? kSat : n1;
+    }
+    cm.mb = cm.ma;
+    if (cm.bb != cm.ba) {
+      float y0 = __uint_as_float(cm.bb), y1 = __uint_as_float(cm.bb | 1u);
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        y0 = __fadd_rn(y0, x[j]);
+        y1 = __fadd_rn(y1, x[j]);
+      }
+      uint32_t n0 = __float_as_uint(y0) - cm.bb, n1 = __float_as_uint(y1) - (cm.bb | 1u);
+      cm.mb.a0 = n0 > kSat ? kSat : n0;
+      cm.mb.a1 = n1 > kSat ? kSat : n1;
+    }
+    maps[q * kThreads + t] = cm;
+  }
+  __syncthreads();
+  // incoming exact sum
+  float c = 0.f;
+  if (sl > 0) {
+    if (!wg_wait_geq(&ws.chain_flag[sl - 1], 1u, s)) *ok = false;
+    c = __hip_atomic_load(&ws.chain_c[sl - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  for (uint32_t q = 0; q < nq; ++q) {
+    const ChainMaps cm = maps[q * kThreads + t];
+    int t0 = 0;
+    for (;;) {
+      const uint32_t cb = __float_as_uint(c);
+      const uint32_t b0 = cb & 0xff800000u;
+      const uint32_t ub = b0 + 0x00800000u;
+      const bool act = t >= t0;
+      PMap m{0u, 0u};
+      bool unknown = false;
+      if (act) {
+        if (b0 == cm.ba) m = cm.ma;
+        else if (b0 == cm.bb) m = cm.mb;
+        else unknown = true;
+      }
+      PMap ex = block_excl_scan(m, s.ecss);
+      const uint32_t par0 = cb & 1u;
+      const uint32_t before = par0 ? ex.a1 : ex.a0;
+      const uint32_t par_t = (par0 ^ before) & 1u;
+      const uint32_t own = par_t ? m.a1 : m.a0;
+      const uint32_t sbits = cb + before;
+      const uint32_t ebits = sbits + own;
+      const bool cross = act && (unknown || before >= kSat || ebits >= ub);
+      unsigned long long bmk = __ballot(cross);
+      if (lane == 0) s.ecss.red_b[w] = bmk ? (w * 64 + __ffsll((long long)bmk) - 1) : kThreads;
+      __syncthreads();
+      int tb = kThreads;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) tb = min(tb, s.ecss.red_b[i]);
+      if (tb == kThreads) {
+        if (t == kThreads - 1) s.ecss.bc_c = __uint_as_float(ebits);
+        __syncthreads();
+        c = s.ecss.bc_c;
+        __syncthreads();
+        break;
+      }
+      if (t == tb) {
+        // exact replay of this thread's segment from its exact start
+        float x[M];
+        chain_load<M>(row, sc, sc.lo + q * chunk + (uint32_t)t * M, m1, x);
+        float y = __uint_as_float(sbits);
+#pragma unroll
+        for (int j = 0; j < M; ++j) y = __fadd_rn(y, expf_glibc(__fsub_rn(x[j], m1)));
+        s.ecss.bc_c = y;
+      }
+      __syncthreads();
+      c = s.ecss.bc_c;
+      __syncthreads();
+      t0 = tb + 1;
+      if (t0 >= kThreads) break;
+    }
+  }
+  if (t == 0) {
+    __hip_atomic_store(&ws.chain_c[sl], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ws.chain_flag[sl], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return c;
+}
+
+// Top-p without top-k or penalties. Pass 1 (all slices): slice max, an
+// exp-sum estimate, and the candidates above a sampled logit threshold.
+// Row barrier. Pass 2: exact T = 1 softmax sum chained across the slices.
+// The last slice then walks the candidates in probability order (window 1 of
+// the reference's sorted order); if the crossing is not inside it, the exact
+// single-workgroup path takes over.
+__device__ void topp_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                           const RowParams& P, const Row& row, RowWs& ws, uint64_t* cand,
+                           float rdraw, Smem& s) {
+  const uint32_t V = a.vocab;
+  const Slice sc = slice_bounds(V, G, sl);
+  if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
+  const uint32_t tau = sample_threshold(row, V, 6000u, s);
+  const float tv = tau ? key2f(tau) : kNegInf;
+  const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
+  float mt = kNegInf;
+  double et = 0.0;
+  uint32_t nan = 0;
+  range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
+    const bool isn = is_nan(v);
+    nan |= isn ? 1u : 0u;
+    if (!isn && v != kNegInf) {
+      if (v > mt) {
+        et = et * (double)__expf(mt - v) + 1.0;
+        mt = v;
+      } else {
+        et += (double)__expf(v - mt);
+      }
+    }
+    cand_push(cand, &ws.cand_n, !isn && (tau == 0u || v >= lo_v),
+              ((uint64_t)(~tkey(v)) << 32) | i);
+  });
+  const float ms = block_rmax(mt, s);
+  nan = block_or_u32(nan, s);
+  double es = (mt == kNegInf) ? 0.0 : et * exp((double)mt - (double)ms);
+  double es_tot;
+  (void)block_excl_scan_f64(es, s, &es_tot);
+  if (threadIdx.x == 0) {
+    ws.part_max[sl] = ms;
+    ws.part_nan[sl] = nan;
+    ws.part_e[sl] = es_tot;
+  }
+  wg_arrive(&ws.bar, s);
+  bool ok = wg_wait_geq(&ws.bar, G, s);
+  float m1 = kNegInf;
+  uint32_t anynan = 0;
+  double p_slice = 0.0;
+  for (uint32_t i = 0; i < G; ++i) {
+    const float mi = ws.part_max[i];
+    m1 = rmax(m1, mi);
+    anynan |= ws.part_nan[i];
+  }
+  for (uint32_t i = 0; i < sl; ++i)
+    if (ws.part_max[i] != kNegInf) p_slice += exp((double)ws.part_max[i] - (double)m1) * ws.part_e[i];
+  const uint32_t ncand = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (!ok || anynan || !is_finite(m1) || ncand > (uint32_t)kCandCap) {
+    // NaN / infinite rows and oversized candidate sets: exact single path
+    if (sl == G - 1u) row_single(a, b, s);
+    return;
+  }
+  const uint32_t len = sc.hi - sc.lo;
+  float S1;
+  if (len <= 16u * kThreads) S1 = slice_chain_sum<16>(row, sc, m1, p_slice, ws, sl, s, &ok);
+  else S1 = slice_chain_sum<32>(row, sc, m1, p_slice, ws, sl, s, &ok);
+  if (sl != G - 1u) return;
+  RowTrace tr;
+  init_trace(tr, V);
+  tr.path = 4u;
+  tr.passes = 2;
+  if (!ok) {
+    tr.status = kStatusListOverflow;
+    write_result(a, b, 0xffffffffu, tr);
+    return;
+  }
+  tr.topp_sum = S1;
+  // window 1: candidates with p >= p(tau)
+  const float p_lo = tau ? __fdiv_rn(expf_glibc(__fsub_rn(tv, m1)), S1) : 0.f;
+  if (threadIdx.x == 0) s.cnt = 0;
+  __syncthreads();
+  for (uint32_t base = 0; base < ncand; base += kThreads) {
+    const uint32_t j = base + threadIdx.x;
+    bool in = false;
+    uint64_t e = 0;
+    if (j < ncand) {
+      const uint64_t c = cand[j];
+      const float v = key2f(~(uint32_t)(c >> 32));
+      const float p = __fdiv_rn(expf_glibc(__fsub_rn(v, m1)), S1);
+      in = p > 0.f && p >= p_lo;
+      e = ((uint64_t)(~__float_as_uint(p)) << 32) | (uint32_t)c;
+    }
+    list_push(s.Bk, &s.cnt, in, e);
+  }
+  __syncthreads();
+  const uint32_t n = s.cnt;
+  sort_u64_asc(s.Bk, n);
+  EcssResult wk = list_ecss(
+      n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe,
+      P.top_p, 0.f, s);
+  if (!wk.found) {
+    row_single(a, b, s);
+    return;
+  }
+  tr.windows = 1;
+  tr.topp_kept = (uint32_t)wk.pos + 1u;
+  tr.topp_cum = wk.c;
+  const uint32_t nk = (uint32_t)wk.pos + 1u;
+  for (uint32_t j = threadIdx.x; j < nk; j += kThreads) {
+    const uint32_t idx = (uint32_t)s.Bk[j];
+    s.A[j] = ((uint64_t)idx << 32) | tkey(row.at(idx));
+  }
+  __syncthreads();
+  sort_u64_asc(s.A, nk);
+  small_path(a, b, P, nk, true, rdraw, s, tr);
+}
+
+extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs a) {
+  __shared__ Smem s;
+  const uint32_t G = a.slices;
+  uint32_t b, sl;
+  if (a.xcd_rows) {
+    // blocks are dispatched to the 8 XCDs round-robin: keep a row's slices on
+    // one XCD so its coordination traffic stays in that XCD's L2
+    const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
+    b = xcd + 8u * (j / G);
+    sl = j % G;
+  } else {
+    b = blockIdx.x / G;
+    sl = blockIdx.x % G;
+  }
+  if (b >= a.batch) return;
+  if (G == 1u) {
+    row_single(a, (int)b, s);
+    return;
+  }
+  const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
+  const float rdraw = a.inline_draws ? a.inline_uniforms[b] : a.uniforms[b];
+  RowWs& ws = a.ws[b];
+  uint64_t* cand = a.cand + (uint64_t)b * kCandCap;
+  const Row row = make_row(a, (int)b);
+  const uint32_t per = ((a.vocab + G - 1u) / G + 15u) & ~15u;
+  if (P.flags & kGreedy) {
+    greedy_split(a, (int)b, sl, G, P, row, ws, s);
+  } else if ((P.flags & kTopK) && P.top_k <= 2048u) {
+    topk_split(a, (int)b, sl, G, P, row, ws, cand, rdraw, s);
+  } else if ((P.flags & kTopP) && !(P.flags & (kTopK | kPen)) && per <= 128u * kThreads) {
+    topp_split(a, (int)b, sl, G, P, row, ws, cand, rdraw, s);
+  } else if (sl == 0) {
+    row_single(a, (int)b, s);
+  }
+  // the last workgroup of the row to leave restores the coordination block
+  const uint32_t old = wg_arrive(&ws.exit_, s);
+  if (old == G - 1u && threadIdx.x == 0) {
+    ws.arrive = 0;
+    ws.bar = 0;
+    ws.cand_n = 0;
+    ws.status = 0;
+    for (uint32_t i = 0; i < G; ++i) ws.chain_flag[i] = 0;
+    __threadfence();
+    ws.exit_ = 0;
+    __threadfence();
+  }
+}
 }  // namespace lumen

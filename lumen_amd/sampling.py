@@ -145,13 +145,14 @@ class Engine:
                      uniforms: Optional[Sequence[float]] = None,
                      rngs: Optional[Sequence[Xorshift64]] = None,
                      penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
-                     sync: bool = True, stream=None):
+                     sync: bool = True, stream=None, uniforms_dev=None):
         """Samples every row of `logits` [B, V].
 
         histories: SamplerState.history per row (the window is applied here),
         or penalty_counts = (offsets, ids, counts) device int32 tensors already
         windowed (the caller-resident SamplerState.freq).
-        uniforms: one draw per row; or rngs: Xorshift64 per row (advanced).
+        uniforms: one draw per row; or rngs: Xorshift64 per row (advanced);
+        or uniforms_dev: a float32 device tensor of draws (no staging copy).
         Returns the token tensor (device); with sync=True also a host list.
         """
         import torch
@@ -183,7 +184,9 @@ class Engine:
             keep += [offs, flat]
             bt.history_offsets = offs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
             bt.history = flat.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
-        if rngs is not None:
+        if uniforms_dev is not None:
+            bt.uniforms_dev = uniforms_dev.data_ptr()
+        elif rngs is not None:
             st = np.array([r.state() for r in rngs], dtype=np.uint64)
             keep.append(st)
             bt.rng_states = st.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
@@ -206,7 +209,7 @@ class Engine:
             rc = L.lumen_sampler_sample_batch_sync(self._h, ctypes.byref(bt), host, s)
         else:
             rc = L.lumen_sampler_sample_batch(self._h, ctypes.byref(bt), s)
-        if rngs is not None:
+        if rngs is not None and uniforms_dev is None:
             for r, v in zip(rngs, st.tolist()):
                 r.set_state(int(v))
         _native.check(rc, "lumen_sampler_sample_batch")

@@ -17,16 +17,23 @@ from lumen_amd.sampling import SamplingParams as SP  # noqa: E402
 from tests import parity  # noqa: E402
 
 
-@pytest.fixture(scope="module")
-def eng():
+@pytest.fixture(scope="module", params=["split", "single"])
+def eng(request):
+    """The engine in its default mode (several workgroups per row) and with
+    one workgroup per row (LUMEN_SAMPLER_SINGLE)."""
     import torch
 
     assert torch.cuda.is_available(), "GPU tests need a GPU"
     from lumen_amd.sampling import Engine
 
+    if request.param == "single":
+        os.environ["LUMEN_SAMPLER_SINGLE"] = "1"
+    else:
+        os.environ.pop("LUMEN_SAMPLER_SINGLE", None)
     e = Engine(0)
     yield e
     e.close()
+    os.environ.pop("LUMEN_SAMPLER_SINGLE", None)
 
 
 def log(*a):
@@ -248,3 +255,42 @@ def test_run_to_run_bit_identity(eng):
         t, h = eng.sample_batch(dev, w.params, histories=w.histories, uniforms=u, trace=tr)
         outs.append((h, tr.cpu().numpy().tobytes()))
     assert outs[0] == outs[1] == outs[2]
+
+
+# ---- the benchmark configurations at full size ------------------------------
+
+def _run_workload(eng, w, n_rows=None, seeds_offset=0):
+    rows = range(w.batch) if n_rows is None else range(n_rows)
+    rows = list(rows)
+    from lumen_amd.sampling import Xorshift64
+
+    u = np.array([Xorshift64(w.seeds[b] + seeds_offset).next_f32() for b in rows], np.float32)
+    lg = w.logits_f32()[rows]
+    params = [w.params[b] for b in rows]
+    hists = [w.histories[b] for b in rows]
+    log(f"case {w.name} rows={len(rows)} V={w.vocab}")
+    if w.dtype == "bf16":
+        rep = parity.compare(eng, lg, params, hists, u, dtype="bf16", bf16_bits=w.logits[rows])
+    else:
+        rep = parity.compare(eng, lg, params, hists, u, check_pen=True)
+    assert_clean(rep, w.name)
+    return rep
+
+
+def test_config1_full(eng):
+    from lumen_amd.workloads import config1, config1_greedy
+
+    _run_workload(eng, config1())
+    _run_workload(eng, config1_greedy())
+
+
+def test_config3_full(eng):
+    from lumen_amd.workloads import config3
+
+    _run_workload(eng, config3())
+
+
+def test_config5_full(eng):
+    from lumen_amd.workloads import config5
+
+    _run_workload(eng, config5(), n_rows=32)
