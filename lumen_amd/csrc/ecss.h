@@ -116,7 +116,7 @@ __device__ __forceinline__ PMap block_excl_scan(PMap v, EcssShared& sh) {
 // finite and >= 0 (zero for padding). `c` is the exact sequential sum of
 // everything before the chunk. Uniform result across the block.
 template <int M>
-__device__ EcssResult ecss_chunk(float c, const float (&x)[M], int mode, float theta,
+__device__ __forceinline__ EcssResult ecss_chunk(float c, const float (&x)[M], int mode, float theta,
                                  EcssShared& sh) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   int t0 = 0;

@@ -35,6 +35,38 @@
 #include "expf_glibc.h"
 #include "kernel_abi.h"
 
+// Development aid: -DLUMEN_TIMING records phase timestamps (100 MHz wall
+// clock) in thread 0 of the finishing workgroup of row 0 and prints them
+// once when that row's result is written.
+#ifdef LUMEN_TIMING
+#include <cstdio>
+__shared__ unsigned long long g_ticks[16];
+__shared__ const char* g_tick_names[16];
+__shared__ int g_nticks;
+#define LUMEN_TICK(label, b)                                         \
+  do {                                                              \
+    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 16) {            \
+      g_ticks[g_nticks] = wall_clock64();                           \
+      g_tick_names[g_nticks++] = label;                             \
+    }                                                               \
+  } while (0)
+#define LUMEN_TICK_INIT() \
+  do {                    \
+    if (threadIdx.x == 0) g_nticks = 0; \
+  } while (0)
+#define LUMEN_TICK_DUMP(b)                                                       \
+  do {                                                                          \
+    if (threadIdx.x == 0 && (b) == 0)                                           \
+      for (int i_ = 1; i_ < g_nticks; ++i_)                                     \
+        printf("tick %s +%f us\n", g_tick_names[i_],                       \
+               (double)(g_ticks[i_] - g_ticks[i_ - 1]) / 100.0);                \
+  } while (0)
+#else
+#define LUMEN_TICK(label, b) do { } while (0)
+#define LUMEN_TICK_INIT() do { } while (0)
+#define LUMEN_TICK_DUMP(b) do { } while (0)
+#endif
+
 namespace lumen {
 
 constexpr int kCap = 8192;          // LDS list capacity (entries)
@@ -151,7 +183,7 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
   return v;
 }
 
-__device__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   v = wave_sum_u32(v);
   if (lane == 0) s.red_a[w] = v;
@@ -163,7 +195,7 @@ __device__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
   return r;
 }
 
-__device__ uint32_t block_or_u32(uint32_t v, Smem& s) {
+__device__ __forceinline__ uint32_t block_or_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
@@ -177,7 +209,7 @@ __device__ uint32_t block_or_u32(uint32_t v, Smem& s) {
 }
 
 // max of a 64-bit value carried as (hi, lo)
-__device__ uint64_t block_max_u64(uint64_t v, Smem& s) {
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -202,7 +234,7 @@ __device__ uint64_t block_max_u64(uint64_t v, Smem& s) {
 }
 
 // fold(-inf, f32::max) over the block; NaN inputs are ignored
-__device__ float block_rmax(float v, Smem& s) {
+__device__ __forceinline__ float block_rmax(float v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = rmax(v, __shfl_xor(v, o, 64));
@@ -215,7 +247,7 @@ __device__ float block_rmax(float v, Smem& s) {
   return r;
 }
 
-__device__ uint32_t block_incl_scan_u32(uint32_t v, Smem& s) {
+__device__ __forceinline__ uint32_t block_incl_scan_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -233,7 +265,7 @@ __device__ uint32_t block_incl_scan_u32(uint32_t v, Smem& s) {
 // Histogram search from the top digit down: returns d with
 // above(d) < need <= above(d) + H[d], above(d) = sum of H over digits > d.
 // d = -1 when the total is below `need` (then *above = total).
-__device__ int find_from_top(const uint32_t* H, int nb, uint32_t need, uint32_t* above, Smem& s) {
+__device__ __forceinline__ int find_from_top(const uint32_t* H, int nb, uint32_t need, uint32_t* above, Smem& s) {
   const int t = threadIdx.x;
   const int per = nb / kThreads;  // 1 or 2
   uint32_t loc = 0;
@@ -263,12 +295,12 @@ __device__ int find_from_top(const uint32_t* H, int nb, uint32_t need, uint32_t*
   return d;
 }
 
-__device__ void clear_hist(uint32_t* H, int nb) {
+__device__ __forceinline__ void clear_hist(uint32_t* H, int nb) {
   for (int i = threadIdx.x; i < nb; i += kThreads) H[i] = 0;
 }
 
 // Ascending bitonic sort of a[0..n) in LDS, padded with ~0.
-__device__ void sort_u64_asc(uint64_t* a, uint32_t n) {
+__device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n) {
   uint32_t np = 2;
   while (np < n) np <<= 1;
   for (uint32_t i = n + threadIdx.x; i < np; i += kThreads) a[i] = ~0ull;
@@ -309,7 +341,7 @@ __device__ __forceinline__ void list_push(uint64_t* list, uint32_t* cnt, bool p,
 // ECSS over a row of V elements, x(i, v) for i < V; 16 contiguous elements
 // per thread per chunk.
 template <class X>
-__device__ EcssResult row_ecss(const Row& r, X&& xf, int mode, float theta, Smem& s) {
+__device__ __attribute__((noinline)) EcssResult row_ecss(const Row& r, X&& xf, int mode, float theta, Smem& s) {
   constexpr int M = 16;
   const uint32_t V = r.V;
   float c = 0.f;
@@ -341,7 +373,7 @@ __device__ EcssResult row_ecss(const Row& r, X&& xf, int mode, float theta, Smem
 
 // ECSS over n elements of an LDS-resident list, x(j) for j < n.
 template <int M, class X>
-__device__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
+__device__ __attribute__((noinline)) EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
   const uint32_t j0 = threadIdx.x * M;
   float x[M];
 #pragma unroll
@@ -350,7 +382,7 @@ __device__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, flo
 }
 
 template <class X>
-__device__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
+__device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
   if (n <= 1024) return list_ecss_m<1>(n, xf, mode, theta, c0, s);
   if (n <= 2048) return list_ecss_m<2>(n, xf, mode, theta, c0, s);
   if (n <= 4096) return list_ecss_m<4>(n, xf, mode, theta, c0, s);
@@ -359,7 +391,7 @@ __device__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float
 
 // Walk over V tokens that all carry the same probability u (the uniform
 // branch of softmax, sampling.rs:211-214 and :224-227).
-__device__ EcssResult const_ecss(uint32_t V, float u, int mode, float theta, Smem& s) {
+__device__ __attribute__((noinline)) EcssResult const_ecss(uint32_t V, float u, int mode, float theta, Smem& s) {
   constexpr int M = 16;
   float c = 0.f;
   for (uint32_t base = 0; base < V; base += (uint32_t)kThreads * M) {
@@ -418,7 +450,9 @@ __device__ __forceinline__ Row make_row(const KernelArgs& a, int b) {
   return row;
 }
 
-__device__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrace& tr) {
+__device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrace& tr) {
+  LUMEN_TICK("write", b);
+  LUMEN_TICK_DUMP(b);
   if (threadIdx.x == 0) {
     a.tokens[b] = token;
     if (a.trace) {
@@ -430,7 +464,7 @@ __device__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrac
 
 // Final stage over the LDS list A (entries (idx << 32) | key, ascending idx,
 // n entries, every entry alive). Applies min-p, temperature, softmax, draw.
-__device__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint32_t n, float r,
+__device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint32_t n, float r,
                                   Smem& s, RowTrace& tr) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
@@ -460,8 +494,10 @@ __device__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint3
   }
   // tokens outside the list are -inf * inv_temp: they only matter when the
   // list has no finite value at all (uniform branch over all V tokens)
+  LUMEN_TICK("fin_m3_local", 0);
   m3 = block_rmax(m3, s);
   nan3 = block_or_u32(nan3, s);
+  LUMEN_TICK("fin_m3_block", 0);
   tr.final_max = m3;
   if (!is_finite(m3)) {
     tr.path |= 16u;
@@ -483,10 +519,12 @@ __device__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint3
   EcssResult S = list_ecss(n, [&](uint32_t j) { return expf_glibc(__fsub_rn(wv(j), m3)); },
                            kEcssSum, 0.f, 0.f, s);
   const float S3 = S.c;
+  LUMEN_TICK("fin_S3", 0);
   tr.final_sum = S3;
   EcssResult e = list_ecss(
       n, [&](uint32_t j) { return __fdiv_rn(expf_glibc(__fsub_rn(wv(j), m3)), S3); },
       kEcssFindGt, r, 0.f, s);
+  LUMEN_TICK("fin_walk", 0);
   tr.cdf_before = e.found ? e.before : e.c;
   tr.cdf_at = e.c;
   if (e.found) return (uint32_t)(s.A[e.pos] >> 32);
@@ -496,7 +534,7 @@ __device__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint3
 // Everything after top-k for a row whose survivors are in s.A as
 // (idx << 32) | key, ascending idx (sampling.rs:502-526): top-p on the list
 // (unless already applied), min-p, temperature, softmax, draw.
-__device__ void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
+__device__ __attribute__((noinline)) void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
                            bool topp_done, float rdraw, Smem& s, RowTrace& tr) {
   const int t = threadIdx.x;
   const uint32_t V = a.vocab;
@@ -589,13 +627,15 @@ __device__ void small_path(const KernelArgs& a, int b, const RowParams& P, uint3
     __syncthreads();
     nlist = nk;
   }
+  LUMEN_TICK("small_before_final", b);
   uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr);
+  LUMEN_TICK("small_after_final", b);
   write_result(a, b, tok, tr);
 }
 
 // The whole sampler for row b, run by one workgroup (used directly when a
 // row has one workgroup, and as the fallback of the split paths).
-__device__ void row_single(const KernelArgs& a, int b, Smem& s) {
+__device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b, Smem& s) {
   const int t = threadIdx.x;
   const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
   const uint32_t V = a.vocab;
@@ -1013,20 +1053,20 @@ __device__ __forceinline__ Slice slice_bounds(uint32_t V, uint32_t G, uint32_t s
 
 // Makes this workgroup's global writes visible at device scope and arrives on
 // *ctr; returns the previous count (uniform across the workgroup).
-__device__ uint32_t wg_arrive(uint32_t* ctr, Smem& s) {
-  __threadfence();
+__device__ __forceinline__ uint32_t wg_arrive(uint32_t* ctr, Smem& s) {
+  // every wave's stores have reached L2 once it passes the barrier; one
+  // device-scope release/acquire by thread 0 then covers the workgroup
   __syncthreads();
   if (threadIdx.x == 0)
     s.misc_u[2] = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   const uint32_t old = s.misc_u[2];
-  __threadfence();
   __syncthreads();
   return old;
 }
 
 // Waits until *ctr >= target (acquire). Returns false on timeout.
-__device__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem& s) {
+__device__ __forceinline__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem& s) {
   if (threadIdx.x == 0) {
     uint32_t n = 0, ok = 1;
     while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
@@ -1040,7 +1080,6 @@ __device__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem& s) {
   }
   __syncthreads();
   const bool ok = s.misc_u[3] != 0;
-  __threadfence();
   __syncthreads();
   return ok;
 }
@@ -1065,7 +1104,7 @@ __device__ __forceinline__ void cand_push(uint64_t* cand, uint32_t* cnt, bool p,
 // Key threshold such that about `target` keys of the row are >= it,
 // estimated from a fixed strided sample, so every workgroup of the row
 // computes the same value. 0 selects everything.
-__device__ uint32_t sample_threshold(const Row& row, uint32_t V, uint32_t target, Smem& s) {
+__device__ __attribute__((noinline)) uint32_t sample_threshold(const Row& row, uint32_t V, uint32_t target, Smem& s) {
   if (V <= kSampleN || target >= V) return 0u;
   const uint32_t r = (uint32_t)(((uint64_t)target * kSampleN + V - 1) / V);
   if (r == 0u || r > kSampleN) return 0u;
@@ -1082,7 +1121,7 @@ __device__ uint32_t sample_threshold(const Row& row, uint32_t V, uint32_t target
 
 // LDS bitmap of the history ids that fall in [lo, hi) (bit i - lo), kept in
 // the Bk area, which is free during slice passes.
-__device__ uint32_t* slice_bitmap(const KernelArgs& a, int b, Slice sc, Smem& s) {
+__device__ __attribute__((noinline)) uint32_t* slice_bitmap(const KernelArgs& a, int b, Slice sc, Smem& s) {
   uint32_t* bm = reinterpret_cast<uint32_t*>(s.Bk);
   const uint32_t nw = (sc.hi - sc.lo + 31u) / 32u;
   for (uint32_t i = threadIdx.x; i < nw; i += kThreads) bm[i] = 0u;
@@ -1101,7 +1140,7 @@ __device__ __forceinline__ bool bm_test(const uint32_t* bm, uint32_t off) {
 }
 
 // Debug copy of the penalized logits of the slice.
-__device__ void slice_pen_out(const KernelArgs& a, int b, const Row& row, Slice sc,
+__device__ __attribute__((noinline)) void slice_pen_out(const KernelArgs& a, int b, const Row& row, Slice sc,
                               const RowParams& P, bool pen) {
   float* po = a.pen_out + (uint64_t)b * a.vocab;
   range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) { po[i] = v; });
@@ -1117,7 +1156,7 @@ __device__ void slice_pen_out(const KernelArgs& a, int b, const Row& row, Slice 
 }
 
 // Greedy: per-slice argmax, the last workgroup to arrive combines.
-__device__ void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+__device__ __attribute__((noinline)) void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
                              const RowParams& P, const Row& row, RowWs& ws, Smem& s) {
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
@@ -1161,7 +1200,7 @@ __device__ void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G
 // candidate buffer, and the last workgroup finishes on the LDS list. If the
 // sample missed (fewer than k or more than the buffer holds), the finisher
 // runs the exact single-workgroup path.
-__device__ void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+__device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
                            const RowParams& P, const Row& row, RowWs& ws, uint64_t* cand,
                            float rdraw, Smem& s) {
   const uint32_t V = a.vocab;
@@ -1170,7 +1209,9 @@ __device__ void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
   const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
+  LUMEN_TICK("topk_start", b + (int)sl);
   const uint32_t tau = sample_threshold(row, V, target, s);
+  LUMEN_TICK("topk_sampled", b + (int)sl);
   const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
   range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
     const uint32_t kk = tkey(v);
@@ -1193,8 +1234,10 @@ __device__ void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
       cand_push(cand, &ws.cand_n, in, ((uint64_t)(~kk) << 32) | id);
     }
   }
+  LUMEN_TICK("topk_compacted", b + (int)sl);
   const uint32_t old = wg_arrive(&ws.arrive, s);
   if (old != G - 1u) return;
+  LUMEN_TICK("topk_finisher", b);
   const uint32_t n = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (n < k || n > (uint32_t)kCandCap) {
     row_single(a, b, s);
@@ -1226,10 +1269,12 @@ __device__ void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
   sort_u64_asc(s.A, ns);  // ascending index
   tr.topk_cutoff_key = cut;
   tr.topk_survivors = ns;
+  LUMEN_TICK("topk_sorted", b);
   small_path(a, b, P, ns, false, rdraw, s, tr);
+  LUMEN_TICK("topk_done", b);
 }
 
-__device__ double block_excl_scan_f64(double v, Smem& s, double* total) {
+__device__ __forceinline__ double block_excl_scan_f64(double v, Smem& s, double* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   double inc = v;
 #pragma unroll
@@ -1285,7 +1330,7 @@ __device__ __forceinline__ void chain_load(const Row& row, Slice sc, uint32_t i0
 }
 
 template <int M>
-__device__ float slice_chain_sum(const Row& row, Slice sc, float m1, double p_slice, RowWs& ws,
+__device__ __attribute__((noinline)) float slice_chain_sum(const Row& row, Slice sc, float m1, double p_slice, RowWs& ws,
                                  uint32_t sl, Smem& s, bool* ok) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const uint32_t chunk = (uint32_t)kThreads * M;
@@ -1407,7 +1452,7 @@ __device__ float slice_chain_sum(const Row& row, Slice sc, float m1, double p_sl
 // The last slice then walks the candidates in probability order (window 1 of
 // the reference's sorted order); if the crossing is not inside it, the exact
 // single-workgroup path takes over.
-__device__ void topp_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+__device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
                            const RowParams& P, const Row& row, RowWs& ws, uint64_t* cand,
                            float rdraw, Smem& s) {
   const uint32_t V = a.vocab;
@@ -1516,8 +1561,16 @@ __device__ void topp_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
   small_path(a, b, P, nk, true, rdraw, s, tr);
 }
 
-extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs a) {
+extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs args) {
+  // Device functions receive the arguments by reference. Referencing the
+  // by-value parameter would make every thread copy it to private memory;
+  // the kernarg segment already holds it (it is the only argument), so the
+  // reference points there instead.
+  (void)args;
+  const KernelArgs& a =
+      *reinterpret_cast<const KernelArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
   __shared__ Smem s;
+  LUMEN_TICK_INIT();
   const uint32_t G = a.slices;
   uint32_t b, sl;
   if (a.xcd_rows) {
