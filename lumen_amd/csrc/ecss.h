@@ -238,4 +238,335 @@ __device__ __forceinline__ EcssResult ecss_chunk(float c, const float (&x)[M], i
   }
 }
 
+// ---------------------------------------------------------------------------
+// Estimate-guided variant: no block scan per binade crossing.
+//
+// ecss_chunk pays one block scan each time the running sum changes binade,
+// and a sum that starts small changes binade dozens of times. Here each
+// thread also has an f64 estimate of the running sum at its start, so the
+// threads whose segment may see a binade change are known in advance
+// ("boundary" threads); every other thread's binade is known and it builds
+// its parity map for that binade only. One segmented block scan (runs of
+// non-boundary threads) composes the maps; then one thread walks the runs
+// and boundaries in order: a run advances the sum through its composed map,
+// a boundary thread is replayed with real f32 adds from its exact start.
+// Every step is checked (the sum must be in the run's binade and must not
+// leave it); a failed check makes the caller fall back to ecss_chunk, so the
+// estimates decide speed only, never the result.
+
+constexpr int kEstMaxB = 128;    // boundary threads per chunk
+constexpr int kEstBx = 1024;     // boundary summands kept in LDS
+constexpr uint32_t kEmptyRun = 0xffffffffu;
+
+struct EstShared {
+  int nb;
+  int fail;
+  int hit_seg;      // search hit inside run hit_seg (-1: none)
+  int hit_pos;      // or at this chunk element, inside a boundary thread (-1: none)
+  float c_out;      // sum after the chunk (or at the hit)
+  float c_seg;      // exact sum at the start of run hit_seg
+  float before;     // sum before the hit element
+  uint32_t wave_head[2 * kWaves];
+  uint32_t wave_lastb[kWaves];
+  uint32_t wave_lastbin[kWaves];
+  uint16_t bpos[kEstMaxB];
+  uint32_t seg_bin[kEstMaxB + 1];
+  PMap seg_tot[kEstMaxB + 1];
+  float bx[kEstBx];
+};
+
+struct SegVal {
+  uint32_t head;  // 1: a boundary thread (runs restart after it)
+  PMap m;
+};
+
+__device__ __forceinline__ SegVal seg_combine(SegVal L, SegVal R) {
+  if (R.head) return R;
+  SegVal o;
+  o.head = L.head;
+  o.m = pm_combine(L.m, R.m);
+  return o;
+}
+
+__device__ __forceinline__ uint32_t est_binade(double x) {
+  float f = __double2float_rz(x > 0.0 ? x : 0.0);
+  return __float_as_uint(f) & 0xff800000u;
+}
+
+__device__ __forceinline__ SegVal shfl_up_seg(SegVal v, int d) {
+  SegVal o;
+  o.head = __shfl_up(v.head, d, 64);
+  o.m.a0 = __shfl_up(v.m.a0, d, 64);
+  o.m.a1 = __shfl_up(v.m.a1, d, 64);
+  return o;
+}
+
+// Inclusive segmented block scan; *prev receives the inclusive value of the
+// previous thread (identity for thread 0).
+__device__ __forceinline__ SegVal seg_scan_incl(SegVal v, EcssShared& sh, EstShared& es,
+                                                SegVal* prev) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  SegVal inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    SegVal L = shfl_up_seg(inc, d);
+    if (lane >= d) inc = seg_combine(L, inc);
+  }
+  if (lane == 63) {
+    sh.wave_tot[w] = inc.m;
+    es.wave_head[w] = inc.head;
+  }
+  __syncthreads();
+  if (w == 0) {
+    SegVal t;
+    t.head = lane < kWaves ? es.wave_head[lane] : 0u;
+    t.m = lane < kWaves ? sh.wave_tot[lane] : PMap{0u, 0u};
+#pragma unroll
+    for (int d = 1; d < kWaves; d <<= 1) {
+      SegVal L = shfl_up_seg(t, d);
+      if (lane >= d) t = seg_combine(L, t);
+    }
+    SegVal ex = shfl_up_seg(t, 1);
+    if (lane == 0) ex = SegVal{0u, PMap{0u, 0u}};
+    if (lane < kWaves) {
+      sh.wave_pre[lane] = ex.m;
+      es.wave_head[kWaves + lane] = ex.head;
+    }
+  }
+  __syncthreads();
+  SegVal pre;
+  pre.head = es.wave_head[kWaves + w];
+  pre.m = sh.wave_pre[w];
+  SegVal in_w = shfl_up_seg(inc, 1);
+  SegVal r = seg_combine(pre, inc);
+  *prev = (lane == 0) ? pre : seg_combine(pre, in_w);
+  __syncthreads();
+  return r;
+}
+
+struct EstThread {
+  uint32_t boundary;
+  uint32_t bin;   // binade base of a non-boundary thread
+  PMap own;       // its parity map for that binade
+  PMap excl;      // composition of its run before it
+  int run;        // index of its run (= boundaries before it)
+};
+
+// Builds runs and boundaries. x: this thread's M summands; p_start / d_self:
+// estimated sum at the thread's start and of its own summands; rel_err: the
+// assumed relative error of p_start. Returns false (uniform) if the result
+// does not fit the LDS budget (the caller then uses ecss_chunk).
+template <int M>
+__device__ __forceinline__ bool est_prepare(const float (&x)[M], double p_start, double d_self,
+                                            double rel_err, EcssShared& sh, EstShared& es,
+                                            EstThread& et) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const uint32_t blo = est_binade(p_start * (1.0 - rel_err));
+  const uint32_t bhi = est_binade((p_start + d_self) * (1.0 + rel_err));
+  et.boundary = blo != bhi ? 1u : 0u;
+  et.bin = blo;
+  et.own = PMap{0u, 0u};
+  if (!et.boundary) {
+    float y0 = __uint_as_float(blo), y1 = __uint_as_float(blo | 1u);
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      y0 = __fadd_rn(y0, x[j]);
+      y1 = __fadd_rn(y1, x[j]);
+    }
+    const uint32_t n0 = __float_as_uint(y0) - blo, n1 = __float_as_uint(y1) - (blo | 1u);
+    et.own.a0 = n0 > kSat ? kSat : n0;
+    et.own.a1 = n1 > kSat ? kSat : n1;
+  }
+  const unsigned long long bm = __ballot(et.boundary != 0u);
+  if (lane == 0) sh.red_b[w] = __popcll(bm);
+  if (lane == 63) {
+    es.wave_lastb[w] = et.boundary;
+    es.wave_lastbin[w] = et.bin;
+  }
+  __syncthreads();
+  int before_w = 0, nb = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    before_w += (i < w) ? sh.red_b[i] : 0;
+    nb += sh.red_b[i];
+  }
+  et.run = before_w + __popcll(bm & ((1ull << lane) - 1ull));
+  SegVal v{et.boundary, et.own};
+  SegVal prev;
+  SegVal inc = seg_scan_incl(v, sh, es, &prev);
+  et.excl = (t == 0) ? PMap{0u, 0u} : prev.m;
+  const bool fits = nb <= kEstMaxB && nb * M <= kEstBx;
+  if (fits) {
+    // predecessor's boundary flag and binade
+    uint32_t pb = __shfl_up(et.boundary, 1, 64), pbin = __shfl_up(et.bin, 1, 64);
+    if (lane == 0 && w > 0) {
+      pb = es.wave_lastb[w - 1];
+      pbin = es.wave_lastbin[w - 1];
+    }
+    if (et.boundary) {
+      const int k = et.run;
+      es.bpos[k] = (uint16_t)t;
+      const bool empty = (t == 0) || pb;
+      es.seg_tot[k] = empty ? PMap{0u, 0u} : prev.m;
+      es.seg_bin[k] = empty ? kEmptyRun : pbin;
+#pragma unroll
+      for (int j = 0; j < M; ++j) es.bx[k * M + j] = x[j];
+    }
+    if (t == kThreads - 1) {
+      es.nb = nb;
+      es.seg_tot[nb] = et.boundary ? PMap{0u, 0u} : inc.m;
+      es.seg_bin[nb] = et.boundary ? kEmptyRun : et.bin;
+    }
+  }
+  __syncthreads();
+  return fits;
+}
+
+// Sequential walk over runs and boundaries (thread 0), then the exact search
+// inside a run when the hit lies there. Returns false (uniform) when a check
+// failed. On success *res holds the chunk result.
+template <int M>
+__device__ __forceinline__ bool est_resolve(float c_in, const float (&x)[M], int mode, float theta,
+                                            const EstThread& et, EcssShared& sh, EstShared& es,
+                                            EcssResult* res) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t == 0) {
+    float c = c_in;
+    int fail = 0, hit_seg = -1, hit_pos = -1;
+    float before = 0.f, cseg = 0.f;
+    const int nb = es.nb;
+    for (int k = 0; k <= nb && !fail && hit_seg < 0 && hit_pos < 0; ++k) {
+      const uint32_t sb = es.seg_bin[k];
+      if (sb != kEmptyRun) {
+        const uint32_t cb = __float_as_uint(c);
+        if ((cb & 0xff800000u) != sb) {
+          fail = 1;
+          break;
+        }
+        const PMap m = es.seg_tot[k];
+        const uint32_t inc = (cb & 1u) ? m.a1 : m.a0;
+        const uint32_t nbits = cb + inc;
+        if (inc >= kSat || nbits >= sb + 0x00800000u) {
+          fail = 1;
+          break;
+        }
+        if (mode != kEcssSum && ecss_cond(mode, __uint_as_float(nbits), theta)) {
+          hit_seg = k;
+          cseg = c;
+          break;
+        }
+        c = __uint_as_float(nbits);
+      }
+      if (k == nb) break;
+      float y = c, p = c;
+      int j = M;
+#pragma unroll
+      for (int q = 0; q < M; ++q) {
+        if (j == M) {
+          p = y;
+          y = __fadd_rn(y, es.bx[k * M + q]);
+          if (mode != kEcssSum && ecss_cond(mode, y, theta)) j = q;
+        }
+      }
+      c = y;
+      if (j < M) {
+        hit_pos = (int)es.bpos[k] * M + j;
+        before = p;
+      }
+    }
+    es.fail = fail;
+    es.hit_seg = hit_seg;
+    es.hit_pos = hit_pos;
+    es.c_out = c;
+    es.c_seg = cseg;
+    es.before = before;
+  }
+  __syncthreads();
+  const int fail = es.fail, hit_seg = es.hit_seg, hit_pos = es.hit_pos;
+  res->c = es.c_out;
+  res->before = es.before;
+  res->found = hit_pos >= 0 ? 1 : 0;
+  res->pos = hit_pos;
+  if (fail) {
+    __syncthreads();
+    return false;
+  }
+  if (hit_seg >= 0) {
+    // exact starts inside the run, then the first thread whose end meets the target
+    const float cs = es.c_seg;
+    const uint32_t cb = __float_as_uint(cs);
+    const bool in = !et.boundary && et.run == hit_seg;
+    uint32_t sbits = 0, ebits = 0;
+    if (in) {
+      const uint32_t b = (cb & 1u) ? et.excl.a1 : et.excl.a0;
+      sbits = cb + b;
+      const uint32_t own = ((cb ^ b) & 1u) ? et.own.a1 : et.own.a0;
+      ebits = sbits + own;
+    }
+    const bool h = in && ecss_cond(mode, __uint_as_float(ebits), theta);
+    const unsigned long long hm = __ballot(h);
+    if (lane == 0) sh.red_h[w] = hm ? (w * 64 + __ffsll((long long)hm) - 1) : kThreads;
+    __syncthreads();
+    int th = kThreads;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) th = min(th, sh.red_h[i]);
+    if (t == th) {
+      float y = __uint_as_float(sbits), p = y;
+      int j = M;
+#pragma unroll
+      for (int q = 0; q < M; ++q) {
+        if (j == M) {
+          p = y;
+          y = __fadd_rn(y, x[q]);
+          if (ecss_cond(mode, y, theta)) j = q;
+        }
+      }
+      es.hit_pos = th * M + j;
+      es.c_out = y;
+      es.before = p;
+    }
+    __syncthreads();
+    res->found = 1;
+    res->pos = es.hit_pos;
+    res->c = es.c_out;
+    res->before = es.before;
+  }
+  __syncthreads();
+  return true;
+}
+
+// Full chunk with the estimate-guided method and the exact fallback. The
+// estimates come from the summands: p(t) = c + sum of the summands before
+// thread t in this chunk, exact enough that only threads within the chunk's
+// worst-case rounding drift of a binade edge become boundaries.
+template <int M>
+__device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[M], int mode,
+                                                      float theta, EcssShared& sh, EstShared& es,
+                                                      double* wsum) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  double d = 0.0;
+#pragma unroll
+  for (int j = 0; j < M; ++j) d += (double)x[j];
+  // exclusive f64 block scan of d
+  double inc = d;
+#pragma unroll
+  for (int k = 1; k < 64; k <<= 1) {
+    double o = __shfl_up(inc, k, 64);
+    if (lane >= k) inc += o;
+  }
+  if (lane == 63) wsum[w] = inc;
+  __syncthreads();
+  double pre = 0.0;
+  for (int i = 0; i < w; ++i) pre += wsum[i];
+  __syncthreads();
+  const double p_start = (double)c + pre + inc - d;
+  const double rel = (double)((t + 1) * M) * 0x1.0p-24 * 1.01 + 1e-9;
+  EstThread et;
+  EcssResult r;
+  if (est_prepare<M>(x, p_start, d, rel, sh, es, et) &&
+      est_resolve<M>(c, x, mode, theta, et, sh, es, &r))
+    return r;
+  return ecss_chunk<M>(c, x, mode, theta, sh);
+}
+
 }  // namespace lumen

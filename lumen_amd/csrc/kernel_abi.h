@@ -58,6 +58,8 @@ enum RowStatus : uint32_t {
 constexpr int kInlineRows = 8;
 constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
 constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
+constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
+constexpr int kEstSharedBytes = 8192;  // upper bound of one parked run structure
 
 // Per-row coordination block in device memory. Zero at allocation; the last
 // workgroup of a row to finish restores the counters to zero, so every
@@ -75,6 +77,7 @@ struct RowWs {
   uint32_t part_nan[kMaxSlices];
   uint64_t part_arg[kMaxSlices];
   double part_e[kMaxSlices];
+  uint32_t part_fits[kMaxSlices];  // bit q: sub-chunk q's run structure is parked
 };
 
 struct KernelArgs {
@@ -97,6 +100,8 @@ struct KernelArgs {
   // Small batches pass their parameters and draws inside the kernel
   // arguments (no staging copy): used when inline_rows > 0.
   RowWs* ws;                 // [B] coordination blocks
+  uint32_t* est;             // [B][kMaxSlices][kChainMaxQ] parked run structures
+                             // (kEstSharedBytes each)
   uint64_t* cand;            // [B][kCandCap] candidate buffers
   uint32_t slices;           // workgroups per row (G)
   uint32_t xcd_rows;         // 1: place all slices of a row on one XCD

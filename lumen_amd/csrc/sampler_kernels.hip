@@ -79,6 +79,8 @@ struct Smem {
   uint32_t H[2048];
   uint32_t H0[2048];
   EcssShared ecss;
+  EstShared est;
+  double wsum[kWaves];
   uint32_t red_a[kWaves];
   uint32_t red_b[kWaves];
   float red_f[kWaves];
@@ -299,28 +301,99 @@ __device__ __forceinline__ void clear_hist(uint32_t* H, int nb) {
   for (int i = threadIdx.x; i < nb; i += kThreads) H[i] = 0;
 }
 
-// Ascending bitonic sort of a[0..n) in LDS, padded with ~0.
+// Key of 0-based rank r in descending order among key(j), j < n (n > r):
+// three LDS histogram rounds over 11/11/10-bit digits.
+template <class K>
+__device__ __forceinline__ uint32_t select_desc(uint32_t n, K&& key, uint32_t r, Smem& s) {
+  uint32_t prefix = 0, pmask = 0, need = r + 1u;
+  for (int lvl = 0; lvl < 3; ++lvl) {
+    const int sh = lvl == 0 ? 21 : (lvl == 1 ? 10 : 0);
+    const int nb = lvl == 2 ? 1024 : 2048;
+    const uint32_t dm = (uint32_t)nb - 1u;
+    clear_hist(s.H, nb);
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
+      const uint32_t k = key(j);
+      if ((k & pmask) == prefix) atomicAdd(&s.H[(k >> sh) & dm], 1u);
+    }
+    __syncthreads();
+    uint32_t ab = 0;
+    const int d = find_from_top(s.H, nb, need, &ab, s);
+    need -= ab;
+    prefix |= (uint32_t)d << sh;
+    pmask |= dm << sh;
+  }
+  return prefix;
+}
+
+// Ascending sort of a[0..n) in LDS (keys unique or order among equal keys
+// irrelevant). n <= 256: every key counts the keys below it and is written
+// to its rank (one pass, two barriers). Larger n: bitonic network, one LDS
+// barrier per stage.
 __device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n) {
-  uint32_t np = 2;
+  const uint32_t t = threadIdx.x;
+  if (n <= 256u) {
+    uint64_t mine = 0;
+    uint32_t rank = 0;
+    if (t < n) {
+      mine = a[t];
+      for (uint32_t j = 0; j < n; ++j) {
+        const uint64_t o = a[j];
+        rank += (o < mine || (o == mine && j < t)) ? 1u : 0u;
+      }
+    }
+    __syncthreads();
+    if (t < n) a[rank] = mine;
+    __syncthreads();
+    return;
+  }
+  uint32_t np = 512;
   while (np < n) np <<= 1;
-  for (uint32_t i = n + threadIdx.x; i < np; i += kThreads) a[i] = ~0ull;
+  for (uint32_t i = n + t; i < np; i += kThreads) a[i] = ~0ull;
   __syncthreads();
+  // wave w owns the 512-key chunks w, w + 16, ...; a stage whose partner
+  // distance j is below 512 stays inside a chunk and needs only a
+  // wave-level LDS fence
+  const uint32_t lane = t & 63u, w = t >> 6;
+  const uint32_t nchunks = np / 512u;
   for (uint32_t k = 2; k <= np; k <<= 1) {
     for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t i = threadIdx.x; i < np; i += kThreads) {
-        uint32_t ixj = i ^ j;
-        if (ixj > i) {
-          uint64_t x = a[i], y = a[ixj];
-          bool up = (i & k) == 0;
-          if ((x > y) == up) {
-            a[i] = y;
-            a[ixj] = x;
+      if (j < 512u) {
+        for (uint32_t ch = w; ch < nchunks; ch += kWaves) {
+#pragma unroll
+          for (uint32_t e = 0; e < 8u; ++e) {
+            const uint32_t i = ch * 512u + e * 64u + lane, ixj = i ^ j;
+            if (ixj > i) {
+              const uint64_t x = a[i], y = a[ixj];
+              const bool up = (i & k) == 0;
+              if ((x > y) == up) {
+                a[i] = y;
+                a[ixj] = x;
+              }
+            }
+          }
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+      } else {
+        __syncthreads();
+        for (uint32_t i = t; i < np; i += kThreads) {
+          const uint32_t ixj = i ^ j;
+          if (ixj > i) {
+            const uint64_t x = a[i], y = a[ixj];
+            const bool up = (i & k) == 0;
+            if ((x > y) == up) {
+              a[i] = y;
+              a[ixj] = x;
+            }
           }
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
+  __syncthreads();
 }
 
 // Wave-aggregated append into an LDS list; returns nothing, counts all.
@@ -341,7 +414,7 @@ __device__ __forceinline__ void list_push(uint64_t* list, uint32_t* cnt, bool p,
 // ECSS over a row of V elements, x(i, v) for i < V; 16 contiguous elements
 // per thread per chunk.
 template <class X>
-__device__ __attribute__((noinline)) EcssResult row_ecss(const Row& r, X&& xf, int mode, float theta, Smem& s) {
+__device__ __forceinline__ EcssResult row_ecss(const Row& r, X&& xf, int mode, float theta, Smem& s) {
   constexpr int M = 16;
   const uint32_t V = r.V;
   float c = 0.f;
@@ -356,7 +429,7 @@ __device__ __attribute__((noinline)) EcssResult row_ecss(const Row& r, X&& xf, i
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < V) ? xf(i + j, v[j]) : 0.f;
     }
-    EcssResult e = ecss_chunk<M>(c, x, mode, theta, s.ecss);
+    EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum);
     if (e.found) {
       e.pos += (int)base;
       return e;
@@ -373,16 +446,46 @@ __device__ __attribute__((noinline)) EcssResult row_ecss(const Row& r, X&& xf, i
 
 // ECSS over n elements of an LDS-resident list, x(j) for j < n.
 template <int M, class X>
-__device__ __attribute__((noinline)) EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
+__device__ __forceinline__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
   const uint32_t j0 = threadIdx.x * M;
   float x[M];
 #pragma unroll
   for (int q = 0; q < M; ++q) x[q] = (j0 + q < n) ? xf(j0 + q) : 0.f;
-  return ecss_chunk<M>(c0, x, mode, theta, s.ecss);
+  return ecss_fast_chunk<M>(c0, x, mode, theta, s.ecss, s.est, s.wsum);
 }
 
 template <class X>
 __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
+  if (n <= (uint32_t)kEstBx) {
+    // short lists: the summands go to LDS in parallel and one thread adds
+    // them in order, which is the reference's own loop
+    float* xs = s.est.bx;
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = xf(j);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float c = c0, prev = c0;
+      int pos = -1;
+      for (uint32_t j = 0; j < n; ++j) {
+        prev = c;
+        c = __fadd_rn(c, xs[j]);
+        if (mode != kEcssSum && ecss_cond(mode, c, theta)) {
+          pos = (int)j;
+          break;
+        }
+      }
+      s.est.c_out = c;
+      s.est.before = prev;
+      s.est.hit_pos = pos;
+    }
+    __syncthreads();
+    EcssResult e;
+    e.c = s.est.c_out;
+    e.before = s.est.before;
+    e.pos = s.est.hit_pos;
+    e.found = e.pos >= 0 ? 1 : 0;
+    __syncthreads();
+    return e;
+  }
   if (n <= 1024) return list_ecss_m<1>(n, xf, mode, theta, c0, s);
   if (n <= 2048) return list_ecss_m<2>(n, xf, mode, theta, c0, s);
   if (n <= 4096) return list_ecss_m<4>(n, xf, mode, theta, c0, s);
@@ -391,7 +494,7 @@ __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, fl
 
 // Walk over V tokens that all carry the same probability u (the uniform
 // branch of softmax, sampling.rs:211-214 and :224-227).
-__device__ __attribute__((noinline)) EcssResult const_ecss(uint32_t V, float u, int mode, float theta, Smem& s) {
+__device__ __forceinline__ EcssResult const_ecss(uint32_t V, float u, int mode, float theta, Smem& s) {
   constexpr int M = 16;
   float c = 0.f;
   for (uint32_t base = 0; base < V; base += (uint32_t)kThreads * M) {
@@ -399,7 +502,7 @@ __device__ __attribute__((noinline)) EcssResult const_ecss(uint32_t V, float u, 
     float x[M];
 #pragma unroll
     for (int j = 0; j < M; ++j) x[j] = (i0 + j < V) ? u : 0.f;
-    EcssResult e = ecss_chunk<M>(c, x, mode, theta, s.ecss);
+    EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum);
     if (e.found) {
       e.pos += (int)base;
       return e;
@@ -464,7 +567,7 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
 
 // Final stage over the LDS list A (entries (idx << 32) | key, ascending idx,
 // n entries, every entry alive). Applies min-p, temperature, softmax, draw.
-__device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint32_t n, float r,
+__device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint32_t n, float r,
                                   Smem& s, RowTrace& tr) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
@@ -524,6 +627,7 @@ __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a,
   EcssResult e = list_ecss(
       n, [&](uint32_t j) { return __fdiv_rn(expf_glibc(__fsub_rn(wv(j), m3)), S3); },
       kEcssFindGt, r, 0.f, s);
+  LUMEN_TICK(s.est.fail ? "walk_failed" : "walk_ok", 0);
   LUMEN_TICK("fin_walk", 0);
   tr.cdf_before = e.found ? e.before : e.c;
   tr.cdf_at = e.c;
@@ -534,7 +638,7 @@ __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a,
 // Everything after top-k for a row whose survivors are in s.A as
 // (idx << 32) | key, ascending idx (sampling.rs:502-526): top-p on the list
 // (unless already applied), min-p, temperature, softmax, draw.
-__device__ __attribute__((noinline)) void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
+__device__ __forceinline__ void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
                            bool topp_done, float rdraw, Smem& s, RowTrace& tr) {
   const int t = threadIdx.x;
   const uint32_t V = a.vocab;
@@ -1045,6 +1149,10 @@ struct Slice {
   uint32_t lo, hi;
 };
 
+__device__ __forceinline__ uint32_t sc_len_max(uint32_t V, uint32_t G) {
+  return ((V + G - 1u) / G + 15u) & ~15u;
+}
+
 __device__ __forceinline__ Slice slice_bounds(uint32_t V, uint32_t G, uint32_t sl) {
   uint32_t per = ((V + G - 1u) / G + 15u) & ~15u;
   uint32_t lo = min(V, sl * per), hi = min(V, lo + per);
@@ -1101,27 +1209,42 @@ __device__ __forceinline__ void cand_push(uint64_t* cand, uint32_t* cnt, bool p,
   }
 }
 
+// Appends this workgroup's candidates, gathered in s.A[0..s.cnt) by
+// list_push, to the row's global buffer with a single atomic. The count is
+// always added in full, so an overflow (of LDS or of the buffer) shows up as
+// a total above the capacity.
+__device__ __forceinline__ void flush_candidates(uint64_t* cand, uint32_t* gcnt, Smem& s) {
+  __syncthreads();
+  const uint32_t n = s.cnt;
+  if (threadIdx.x == 0)
+    s.misc_u[1] = n ? __hip_atomic_fetch_add(gcnt, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  __syncthreads();
+  const uint32_t base = s.misc_u[1];
+  const uint32_t m = min(n, (uint32_t)kCap);
+  for (uint32_t j = threadIdx.x; j < m; j += kThreads)
+    if (base + j < (uint32_t)kCandCap) cand[base + j] = s.A[j];
+  __syncthreads();
+}
+
 // Key threshold such that about `target` keys of the row are >= it,
 // estimated from a fixed strided sample, so every workgroup of the row
 // computes the same value. 0 selects everything.
-__device__ __attribute__((noinline)) uint32_t sample_threshold(const Row& row, uint32_t V, uint32_t target, Smem& s) {
+__device__ __forceinline__ uint32_t sample_threshold(const Row& row, uint32_t V, uint32_t target, Smem& s) {
   if (V <= kSampleN || target >= V) return 0u;
   const uint32_t r = (uint32_t)(((uint64_t)target * kSampleN + V - 1) / V);
   if (r == 0u || r > kSampleN) return 0u;
-  for (uint32_t j = threadIdx.x; j < kSampleN; j += kThreads) {
-    uint32_t i = (uint32_t)(((uint64_t)j * V) / kSampleN);
-    s.A[j] = (uint64_t)(~tkey(row.at(i))) << 32;
-  }
+  uint32_t* keys = reinterpret_cast<uint32_t*>(s.A);
+  for (uint32_t j = threadIdx.x; j < kSampleN; j += kThreads)
+    keys[j] = tkey(row.at((uint32_t)(((uint64_t)j * V) / kSampleN)));
   __syncthreads();
-  sort_u64_asc(s.A, kSampleN);
-  const uint32_t tau = ~(uint32_t)(s.A[r - 1] >> 32);
+  const uint32_t tau = select_desc(kSampleN, [&](uint32_t j) { return keys[j]; }, r - 1u, s);
   __syncthreads();
   return tau;
 }
 
 // LDS bitmap of the history ids that fall in [lo, hi) (bit i - lo), kept in
 // the Bk area, which is free during slice passes.
-__device__ __attribute__((noinline)) uint32_t* slice_bitmap(const KernelArgs& a, int b, Slice sc, Smem& s) {
+__device__ __forceinline__ uint32_t* slice_bitmap(const KernelArgs& a, int b, Slice sc, Smem& s) {
   uint32_t* bm = reinterpret_cast<uint32_t*>(s.Bk);
   const uint32_t nw = (sc.hi - sc.lo + 31u) / 32u;
   for (uint32_t i = threadIdx.x; i < nw; i += kThreads) bm[i] = 0u;
@@ -1140,7 +1263,7 @@ __device__ __forceinline__ bool bm_test(const uint32_t* bm, uint32_t off) {
 }
 
 // Debug copy of the penalized logits of the slice.
-__device__ __attribute__((noinline)) void slice_pen_out(const KernelArgs& a, int b, const Row& row, Slice sc,
+__device__ __forceinline__ void slice_pen_out(const KernelArgs& a, int b, const Row& row, Slice sc,
                               const RowParams& P, bool pen) {
   float* po = a.pen_out + (uint64_t)b * a.vocab;
   range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) { po[i] = v; });
@@ -1213,10 +1336,12 @@ __device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b,
   const uint32_t tau = sample_threshold(row, V, target, s);
   LUMEN_TICK("topk_sampled", b + (int)sl);
   const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
+  if (threadIdx.x == 0) s.cnt = 0;
+  __syncthreads();
   range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
     const uint32_t kk = tkey(v);
     const bool in = kk >= tau && !(pen && bm_test(bm, i - sc.lo));
-    cand_push(cand, &ws.cand_n, in, ((uint64_t)(~kk) << 32) | i);
+    list_push(s.A, &s.cnt, in, ((uint64_t)(~kk) << 32) | i);
   });
   if (pen) {
     const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
@@ -1231,9 +1356,10 @@ __device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b,
           in = kk >= tau;
         }
       }
-      cand_push(cand, &ws.cand_n, in, ((uint64_t)(~kk) << 32) | id);
+      list_push(s.A, &s.cnt, in, ((uint64_t)(~kk) << 32) | id);
     }
   }
+  flush_candidates(cand, &ws.cand_n, s);
   LUMEN_TICK("topk_compacted", b + (int)sl);
   const uint32_t old = wg_arrive(&ws.arrive, s);
   if (old != G - 1u) return;
@@ -1248,23 +1374,44 @@ __device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b,
   tr.passes = 1;
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) s.A[j] = cand[j];
   __syncthreads();
-  sort_u64_asc(s.A, n);  // descending key, then ascending index
-  uint32_t ns;
-  uint32_t cut;
+  LUMEN_TICK("topk_loaded", b);
+  // candidate entries are (~key << 32) | idx
+  auto ckey = [&](uint32_t j) { return ~(uint32_t)(s.A[j] >> 32); };
+  uint32_t cut, ns;
   if (k == 1) {
     // sampling.rs:913-921: exactly the lowest-index maximum
+    uint64_t best = 0;
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
+      const uint64_t e = s.A[j];
+      const uint64_t kk = ((uint64_t)(~(uint32_t)(e >> 32)) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+      best = kk > best ? kk : best;
+    }
+    best = block_max_u64(best, s);
+    cut = (uint32_t)(best >> 32);
+    if (threadIdx.x == 0) s.Bk[0] = ((uint64_t)(0xffffffffu - (uint32_t)best) << 32) | cut;
     ns = 1;
-    cut = ~(uint32_t)(s.A[0] >> 32);
+    __syncthreads();
   } else {
-    cut = ~(uint32_t)(s.A[k - 1] >> 32);
-    uint32_t c = 0;
-    for (uint32_t j = threadIdx.x; j < n; j += kThreads) c += (~(uint32_t)(s.A[j] >> 32) >= cut) ? 1u : 0u;
-    ns = block_sum_u32(c, s);
+    cut = select_desc(n, ckey, k - 1u, s);
+    // survivors (every key >= cut, ties included) as (idx << 32) | key
+    if (threadIdx.x == 0) s.cnt = 0;
+    __syncthreads();
+    for (uint32_t base = 0; base < n; base += kThreads) {
+      const uint32_t j = base + threadIdx.x;
+      bool in = false;
+      uint64_t e = 0;
+      if (j < n) {
+        const uint32_t kk = ckey(j);
+        in = kk >= cut;
+        e = ((uint64_t)(uint32_t)s.A[j] << 32) | kk;
+      }
+      list_push(s.Bk, &s.cnt, in, e);
+    }
+    __syncthreads();
+    ns = s.cnt;
   }
-  for (uint32_t j = threadIdx.x; j < ns; j += kThreads) {
-    uint64_t e = s.A[j];
-    s.A[j] = ((uint64_t)(uint32_t)e << 32) | (uint64_t)(~(uint32_t)(e >> 32));
-  }
+  LUMEN_TICK("topk_sort1", b);
+  for (uint32_t j = threadIdx.x; j < ns; j += kThreads) s.A[j] = s.Bk[j];
   __syncthreads();
   sort_u64_asc(s.A, ns);  // ascending index
   tr.topk_cutoff_key = cut;
@@ -1301,20 +1448,16 @@ __device__ __forceinline__ uint32_t binade_bits(double x) {
   return __float_as_uint(f) & 0xff800000u;
 }
 
-// Exact sequential f32 sum of expf(v - m1) over slice [lo, hi), continuing
-// the running sum of the slices before it. The slice is cut into sub-chunks
-// of kThreads * M elements; in each, thread t owns M consecutive elements.
-// Before waiting for the previous slice, every thread computes its
-// summands, a f64 estimate of the running sum at its start, and the parity
-// maps for the one or two binades that sum can be in; the maps are parked in
-// LDS (the list area is idle in this phase). After the wait only block scans
-// remain, plus an exact replay (summands recomputed) of each thread in which
-// the running sum changes binade. Publishes the outgoing sum in
-// ws.chain_c[sl].
-struct ChainMaps {
-  uint32_t ba, bb;  // binade bases (f32 bits) the maps were built for
-  PMap ma, mb;
-};
+// Exact T = 1 softmax sum across the slices of a row, without a chain of
+// waits. Each workgroup cuts its slice into sub-chunks of kThreads * M
+// elements (thread t owns M consecutive ones), computes the summands and an
+// f64 estimate of the running sum at every thread (its slice's estimated
+// prefix plus the summands before it), builds the run/boundary structure of
+// est_prepare and parks it in device memory. The last workgroup to arrive
+// then walks all structures in row order (est_resolve), exactly; a
+// sub-chunk whose structure failed a check is recomputed and summed by the
+// iterative method instead.
+static_assert(sizeof(EstShared) <= (size_t)kEstSharedBytes, "parked run structure too large");
 
 template <int M>
 __device__ __forceinline__ void chain_load(const Row& row, Slice sc, uint32_t i0, float m1,
@@ -1325,123 +1468,85 @@ __device__ __forceinline__ void chain_load(const Row& row, Slice sc, uint32_t i0
     const uint32_t i = i0 + 4u * q;
     if (i < sc.hi) row.load4(i, v);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < sc.hi) ? v[j] : kNegInf;
+    for (int j = 0; j < 4; ++j) x[4 * q + j] = expf_glibc(__fsub_rn((i + j < sc.hi) ? v[j] : kNegInf, m1));
   }
 }
 
+__device__ __forceinline__ uint32_t* est_slot(const KernelArgs& a, int b, uint32_t sl, uint32_t q) {
+  return a.est + (((uint64_t)b * kMaxSlices + sl) * kChainMaxQ + q) * (kEstSharedBytes / 4);
+}
+
+__device__ __forceinline__ void copy_words(uint32_t* dst, const uint32_t* src, uint32_t nw) {
+  for (uint32_t i = threadIdx.x; i < nw; i += kThreads) dst[i] = src[i];
+}
+
 template <int M>
-__device__ __attribute__((noinline)) float slice_chain_sum(const Row& row, Slice sc, float m1, double p_slice, RowWs& ws,
-                                 uint32_t sl, Smem& s, bool* ok) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+__device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, uint32_t sl,
+                                                  const Row& row, Slice sc, float m1,
+                                                  double p_slice, Smem& s) {
   const uint32_t chunk = (uint32_t)kThreads * M;
-  const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;  // <= 4 (LDS map budget)
-  ChainMaps* maps = reinterpret_cast<ChainMaps*>(s.A);
+  const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;
+  const uint32_t nw = (uint32_t)((sizeof(EstShared) + 3) / 4);
+  uint32_t fits = 0;
   double pre = p_slice;
   for (uint32_t q = 0; q < nq; ++q) {
-    const uint32_t i0 = sc.lo + q * chunk + (uint32_t)t * M;
+    const uint32_t i0 = sc.lo + q * chunk + (uint32_t)threadIdx.x * M;
     float x[M];
     chain_load<M>(row, sc, i0, m1, x);
     double d = 0.0;
 #pragma unroll
-    for (int j = 0; j < M; ++j) d += (double)__expf(x[j] - m1);
+    for (int j = 0; j < M; ++j) d += (double)x[j];
     double tot;
     const double pt = pre + block_excl_scan_f64(d, s, &tot);
     pre += tot;
-#pragma unroll
-    for (int j = 0; j < M; ++j) x[j] = expf_glibc(__fsub_rn(x[j], m1));
-    // |C - P| <= (elements before) * 2^-24 * C for a sequential f32 sum of
-    // non-negative terms; 1e-5 covers the estimate's own error
-    const double eps = (double)i0 * 0x1.0p-24 * 1.01 + 1e-5;
-    ChainMaps cm;
-    cm.ba = binade_bits(pt * (1.0 - eps));
-    cm.bb = binade_bits(pt * (1.0 + eps));
-    {
-      float y0 = __uint_as_float(cm.ba), y1 = __uint_as_float(cm.ba | 1u);
-#pragma unroll
-      for (int j = 0; j < M; ++j) {
-        y0 = __fadd_rn(y0, x[j]);
-        y1 = __fadd_rn(y1, x[j]);
-      }
-      uint32_t n0 = __float_as_uint(y0) - cm.ba, n1 = __float_as_uint(y1) - (cm.ba | 1u);
-      cm.ma.a0 = n0 > kSat ? kSat : n0;
-      cm.ma.a1 = n1 > kSat ? kSat : n1;
+    // The incoming sum is only estimated here (other slices' exp-sums); the
+    // rounding drift of a long f32 sum is typically ~1e-5 relative. A wrong
+    // guess only costs the exact recomputation in chain_walk.
+    EstThread et;
+    if (est_prepare<M>(x, pt, d, 4e-5, s.ecss, s.est, et)) {
+      fits |= 1u << q;
+      copy_words(est_slot(a, b, sl, q), reinterpret_cast<const uint32_t*>(&s.est), nw);
     }
-    cm.mb = cm.ma;
-    if (cm.bb != cm.ba) {
-      float y0 = __uint_as_float(cm.bb), y1 = __uint_as_float(cm.bb | 1u);
-#pragma unroll
-      for (int j = 0; j < M; ++j) {
-        y0 = __fadd_rn(y0, x[j]);
-        y1 = __fadd_rn(y1, x[j]);
-      }
-      uint32_t n0 = __float_as_uint(y0) - cm.bb, n1 = __float_as_uint(y1) - (cm.bb | 1u);
-      cm.mb.a0 = n0 > kSat ? kSat : n0;
-      cm.mb.a1 = n1 > kSat ? kSat : n1;
-    }
-    maps[q * kThreads + t] = cm;
+    __syncthreads();
   }
-  __syncthreads();
-  // incoming exact sum
-  float c = 0.f;
-  if (sl > 0) {
-    if (!wg_wait_geq(&ws.chain_flag[sl - 1], 1u, s)) *ok = false;
-    c = __hip_atomic_load(&ws.chain_c[sl - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  return fits;
+}
+
+// Number of EstShared structures that fit in the LDS list area (A and Bk).
+constexpr uint32_t kParkedInLds = (uint32_t)(2u * kCap * sizeof(uint64_t) / sizeof(EstShared));
+
+template <int M>
+__device__ __forceinline__ float chain_walk_slice(const KernelArgs& a, int b, uint32_t sl,
+                                                  const Row& row, Slice sc, float m1,
+                                                  uint32_t fits, float c, Smem& s) {
+  const uint32_t chunk = (uint32_t)kThreads * M;
+  const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;
+  const uint32_t nw = (uint32_t)((sizeof(EstShared) + 3) / 4);
   for (uint32_t q = 0; q < nq; ++q) {
-    const ChainMaps cm = maps[q * kThreads + t];
-    int t0 = 0;
-    for (;;) {
-      const uint32_t cb = __float_as_uint(c);
-      const uint32_t b0 = cb & 0xff800000u;
-      const uint32_t ub = b0 + 0x00800000u;
-      const bool act = t >= t0;
-      PMap m{0u, 0u};
-      bool unknown = false;
-      if (act) {
-        if (b0 == cm.ba) m = cm.ma;
-        else if (b0 == cm.bb) m = cm.mb;
-        else unknown = true;
-      }
-      PMap ex = block_excl_scan(m, s.ecss);
-      const uint32_t par0 = cb & 1u;
-      const uint32_t before = par0 ? ex.a1 : ex.a0;
-      const uint32_t par_t = (par0 ^ before) & 1u;
-      const uint32_t own = par_t ? m.a1 : m.a0;
-      const uint32_t sbits = cb + before;
-      const uint32_t ebits = sbits + own;
-      const bool cross = act && (unknown || before >= kSat || ebits >= ub);
-      unsigned long long bmk = __ballot(cross);
-      if (lane == 0) s.ecss.red_b[w] = bmk ? (w * 64 + __ffsll((long long)bmk) - 1) : kThreads;
-      __syncthreads();
-      int tb = kThreads;
-#pragma unroll
-      for (int i = 0; i < kWaves; ++i) tb = min(tb, s.ecss.red_b[i]);
-      if (tb == kThreads) {
-        if (t == kThreads - 1) s.ecss.bc_c = __uint_as_float(ebits);
+    bool done = false;
+    if ((fits >> q) & 1u) {
+      // the finisher copied the first kParkedInLds parked structures into the list area
+      const uint32_t slot = sl * kChainMaxQ + q;
+      EstShared* es = slot < kParkedInLds ? reinterpret_cast<EstShared*>(s.A) + slot : &s.est;
+      if (slot >= kParkedInLds) {
+        copy_words(reinterpret_cast<uint32_t*>(&s.est), est_slot(a, b, sl, q), nw);
         __syncthreads();
-        c = s.ecss.bc_c;
-        __syncthreads();
-        break;
       }
-      if (t == tb) {
-        // exact replay of this thread's segment from its exact start
-        float x[M];
-        chain_load<M>(row, sc, sc.lo + q * chunk + (uint32_t)t * M, m1, x);
-        float y = __uint_as_float(sbits);
+      float xz[M];
 #pragma unroll
-        for (int j = 0; j < M; ++j) y = __fadd_rn(y, expf_glibc(__fsub_rn(x[j], m1)));
-        s.ecss.bc_c = y;
+      for (int j = 0; j < M; ++j) xz[j] = 0.f;
+      EstThread et{};
+      EcssResult r;
+      if (est_resolve<M>(c, xz, kEcssSum, 0.f, et, s.ecss, *es, &r)) {
+        c = r.c;
+        done = true;
       }
-      __syncthreads();
-      c = s.ecss.bc_c;
-      __syncthreads();
-      t0 = tb + 1;
-      if (t0 >= kThreads) break;
     }
-  }
-  if (t == 0) {
-    __hip_atomic_store(&ws.chain_c[sl], c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&ws.chain_flag[sl], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (!done) {
+      float x[M];
+      chain_load<M>(row, sc, sc.lo + q * chunk + (uint32_t)threadIdx.x * M, m1, x);
+      c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
+    }
   }
   return c;
 }
@@ -1458,12 +1563,16 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
+  LUMEN_TICK("p_start", b + (int)sl - (int)(G - 1u));
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
+  LUMEN_TICK("p_sampled", b + (int)sl - (int)(G - 1u));
   const float tv = tau ? key2f(tau) : kNegInf;
   const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
   float mt = kNegInf;
   double et = 0.0;
   uint32_t nan = 0;
+  if (threadIdx.x == 0) s.cnt = 0;
+  __syncthreads();
   range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
     const bool isn = is_nan(v);
     nan |= isn ? 1u : 0u;
@@ -1475,9 +1584,9 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
         et += (double)__expf(v - mt);
       }
     }
-    cand_push(cand, &ws.cand_n, !isn && (tau == 0u || v >= lo_v),
-              ((uint64_t)(~tkey(v)) << 32) | i);
+    list_push(s.A, &s.cnt, !isn && (tau == 0u || v >= lo_v), ((uint64_t)(~tkey(v)) << 32) | i);
   });
+  flush_candidates(cand, &ws.cand_n, s);
   const float ms = block_rmax(mt, s);
   nan = block_or_u32(nan, s);
   double es = (mt == kNegInf) ? 0.0 : et * exp((double)mt - (double)ms);
@@ -1488,8 +1597,12 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
     ws.part_nan[sl] = nan;
     ws.part_e[sl] = es_tot;
   }
+  LUMEN_TICK("p_pass1", b + (int)sl - (int)(G - 1u));
   wg_arrive(&ws.bar, s);
-  bool ok = wg_wait_geq(&ws.bar, G, s);
+  const bool ok = wg_wait_geq(&ws.bar, G, s);
+  if (!ok && threadIdx.x == 0)
+    __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  LUMEN_TICK("p_barrier", b + (int)sl - (int)(G - 1u));
   float m1 = kNegInf;
   uint32_t anynan = 0;
   double p_slice = 0.0;
@@ -1501,25 +1614,47 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
   for (uint32_t i = 0; i < sl; ++i)
     if (ws.part_max[i] != kNegInf) p_slice += exp((double)ws.part_max[i] - (double)m1) * ws.part_e[i];
   const uint32_t ncand = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (!ok || anynan || !is_finite(m1) || ncand > (uint32_t)kCandCap) {
-    // NaN / infinite rows and oversized candidate sets: exact single path
-    if (sl == G - 1u) row_single(a, b, s);
+  // NaN / infinite rows and oversized candidate sets take the exact single
+  // path (uniform across the row once the barrier has completed)
+  const bool single = anynan || !is_finite(m1) || ncand > (uint32_t)kCandCap;
+  const bool m16 = sc_len_max(V, G) <= 16u * kThreads;
+  uint32_t fits = 0;
+  if (ok && !single)
+    fits = m16 ? chain_prepare<16>(a, b, sl, row, sc, m1, p_slice, s)
+               : chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
+  if (threadIdx.x == 0) ws.part_fits[sl] = fits;
+  LUMEN_TICK("p_prepared", b + (int)sl - (int)(G - 1u));
+  if (wg_arrive(&ws.arrive, s) != G - 1u) return;
+  LUMEN_TICK("p_finisher", b);
+  if (!ok || single ||
+      __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+    row_single(a, b, s);
     return;
   }
-  const uint32_t len = sc.hi - sc.lo;
-  float S1;
-  if (len <= 16u * kThreads) S1 = slice_chain_sum<16>(row, sc, m1, p_slice, ws, sl, s, &ok);
-  else S1 = slice_chain_sum<32>(row, sc, m1, p_slice, ws, sl, s, &ok);
-  if (sl != G - 1u) return;
+  {
+    // bring every parked structure of the row into LDS with one bulk copy
+    const uint32_t nw = (uint32_t)((sizeof(EstShared) + 3) / 4);
+    const uint32_t nslots = min(G * (uint32_t)kChainMaxQ, kParkedInLds);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(s.A);
+    for (uint32_t x = threadIdx.x; x < nslots * nw; x += kThreads) {
+      const uint32_t slot = x / nw, word = x - slot * nw;
+      dst[slot * (uint32_t)(sizeof(EstShared) / 4) + word] =
+          est_slot(a, b, slot / kChainMaxQ, slot % kChainMaxQ)[word];
+    }
+    __syncthreads();
+  }
+  float S1 = 0.f;
+  for (uint32_t i = 0; i < G; ++i) {
+    const Slice si = slice_bounds(V, G, i);
+    const uint32_t fi = __hip_atomic_load(&ws.part_fits[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    S1 = m16 ? chain_walk_slice<16>(a, b, i, row, si, m1, fi, S1, s)
+             : chain_walk_slice<32>(a, b, i, row, si, m1, fi, S1, s);
+  }
+  LUMEN_TICK("p_chain", b);
   RowTrace tr;
   init_trace(tr, V);
   tr.path = 4u;
   tr.passes = 2;
-  if (!ok) {
-    tr.status = kStatusListOverflow;
-    write_result(a, b, 0xffffffffu, tr);
-    return;
-  }
   tr.topp_sum = S1;
   // window 1: candidates with p >= p(tau)
   const float p_lo = tau ? __fdiv_rn(expf_glibc(__fsub_rn(tv, m1)), S1) : 0.f;
@@ -1540,10 +1675,13 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
   }
   __syncthreads();
   const uint32_t n = s.cnt;
+  LUMEN_TICK("p_window_built", b);
   sort_u64_asc(s.Bk, n);
+  LUMEN_TICK("p_window_sorted", b);
   EcssResult wk = list_ecss(
       n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe,
       P.top_p, 0.f, s);
+  LUMEN_TICK("p_walked", b);
   if (!wk.found) {
     row_single(a, b, s);
     return;
@@ -1558,6 +1696,7 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
   }
   __syncthreads();
   sort_u64_asc(s.A, nk);
+  LUMEN_TICK("p_kept_sorted", b);
   small_path(a, b, P, nk, true, rdraw, s, tr);
 }
 
@@ -1584,6 +1723,21 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
     sl = blockIdx.x % G;
   }
   if (b >= a.batch) return;
+#ifdef LUMEN_GREEDY_ONLY
+  {
+    const Row row = make_row(a, (int)b);
+    const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
+    uint64_t best = 0;
+    row_foreach(row, [&](uint32_t i, float v) {
+      uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+      best = k > best ? k : best;
+    });
+    best = block_max_u64(best, s);
+    if (threadIdx.x == 0) a.tokens[b] = 0xffffffffu - (uint32_t)best;
+    (void)P;
+    return;
+  }
+#endif
   if (G == 1u) {
     row_single(a, (int)b, s);
     return;
@@ -1598,7 +1752,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
     greedy_split(a, (int)b, sl, G, P, row, ws, s);
   } else if ((P.flags & kTopK) && P.top_k <= 2048u) {
     topk_split(a, (int)b, sl, G, P, row, ws, cand, rdraw, s);
-  } else if ((P.flags & kTopP) && !(P.flags & (kTopK | kPen)) && per <= 128u * kThreads) {
+  } else if ((P.flags & kTopP) && !(P.flags & (kTopK | kPen)) && per <= 32u * kThreads * kChainMaxQ) {
     topp_split(a, (int)b, sl, G, P, row, ws, cand, rdraw, s);
   } else if (sl == 0) {
     row_single(a, (int)b, s);
