@@ -359,11 +359,13 @@ struct EstThread {
 template <int M>
 __device__ __forceinline__ bool est_prepare(const float (&x)[M], double p_start, double d_self,
                                             double rel_err, EcssShared& sh, EstShared& es,
-                                            EstThread& et) {
+                                            EstThread& et, int nact = kThreads) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const uint32_t blo = est_binade(p_start * (1.0 - rel_err));
   const uint32_t bhi = est_binade((p_start + d_self) * (1.0 + rel_err));
-  et.boundary = blo != bhi ? 1u : 0u;
+  // threads from nact on hold only zero padding: identity maps, never
+  // boundaries, and the last run ends at thread nact - 1
+  et.boundary = (blo != bhi && t < nact) ? 1u : 0u;
   et.bin = blo;
   et.own = PMap{0u, 0u};
   if (!et.boundary) {
@@ -412,7 +414,7 @@ __device__ __forceinline__ bool est_prepare(const float (&x)[M], double p_start,
 #pragma unroll
       for (int j = 0; j < M; ++j) es.bx[k * M + j] = x[j];
     }
-    if (t == kThreads - 1) {
+    if (t == nact - 1) {
       es.nb = nb;
       es.seg_tot[nb] = et.boundary ? PMap{0u, 0u} : inc.m;
       es.seg_bin[nb] = et.boundary ? kEmptyRun : et.bin;
@@ -542,7 +544,7 @@ __device__ __forceinline__ bool est_resolve(float c_in, const float (&x)[M], int
 template <int M>
 __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[M], int mode,
                                                       float theta, EcssShared& sh, EstShared& es,
-                                                      double* wsum) {
+                                                      double* wsum, int nact = kThreads) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   double d = 0.0;
 #pragma unroll
@@ -563,9 +565,11 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
   const double rel = (double)((t + 1) * M) * 0x1.0p-24 * 1.01 + 1e-9;
   EstThread et;
   EcssResult r;
-  if (est_prepare<M>(x, p_start, d, rel, sh, es, et) &&
-      est_resolve<M>(c, x, mode, theta, et, sh, es, &r))
-    return r;
+  if (!est_prepare<M>(x, p_start, d, rel, sh, es, et, nact)) {
+    if (t == 0) es.fail = 2;  // structure did not fit (diagnostic only)
+    return ecss_chunk<M>(c, x, mode, theta, sh);
+  }
+  if (est_resolve<M>(c, x, mode, theta, et, sh, es, &r)) return r;
   return ecss_chunk<M>(c, x, mode, theta, sh);
 }
 

@@ -40,12 +40,12 @@
 // once when that row's result is written.
 #ifdef LUMEN_TIMING
 #include <cstdio>
-__shared__ unsigned long long g_ticks[16];
-__shared__ const char* g_tick_names[16];
+__shared__ unsigned long long g_ticks[48];
+__shared__ const char* g_tick_names[48];
 __shared__ int g_nticks;
 #define LUMEN_TICK(label, b)                                         \
   do {                                                              \
-    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 16) {            \
+    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 48) {            \
       g_ticks[g_nticks] = wall_clock64();                           \
       g_tick_names[g_nticks++] = label;                             \
     }                                                               \
@@ -76,8 +76,8 @@ constexpr float kNegInf = -__builtin_huge_valf();
 struct Smem {
   uint64_t A[kCap];
   uint64_t Bk[kCap];
-  uint32_t H[2048];
-  uint32_t H0[2048];
+  uint32_t H[4096];   // histograms (radix sort: 256 digits x 16 waves)
+  uint32_t H0[2048];  // window planner histogram, kept across windows
   EcssShared ecss;
   EstShared est;
   double wsum[kWaves];
@@ -326,11 +326,131 @@ __device__ __forceinline__ uint32_t select_desc(uint32_t n, K&& key, uint32_t r,
   return prefix;
 }
 
+// Lanes of the wave whose 8-bit digit equals this lane's (among `valid`).
+__device__ __forceinline__ uint64_t match_digit8(uint32_t d, bool valid) {
+  uint64_t m = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (d >> b) & 1u;
+    const uint64_t bb = __ballot(bit);
+    m &= bit ? bb : ~bb;
+  }
+  return m;
+}
+
+// One stable counting pass on the 8-bit digit at `shift`: src -> dst. Wave w
+// owns the contiguous range [w * per_w, (w + 1) * per_w) and walks it in
+// 64-entry tiles; the 256 x 16 counters (digit-major, wave-minor) are
+// scanned so that equal digits keep wave order, tile order and lane order.
+__device__ __forceinline__ void radix_pass(const uint64_t* src, uint64_t* dst, uint32_t n,
+                                           uint32_t shift, Smem& s) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  uint32_t* hist = s.H;
+  const uint32_t per_w = ((n + kThreads - 1u) / kThreads) * 64u;
+  const uint32_t wlo = min(n, w * per_w), whi = min(n, wlo + per_w);
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (uint32_t i = t; i < 4096u; i += kThreads) hist[i] = 0u;
+  __syncthreads();
+  // only this wave touches column w, and the leaders of one tile hold
+  // distinct digits: plain LDS read-modify-writes suffice
+  for (uint32_t base = wlo; base < whi; base += 64u) {
+    const uint32_t i = base + lane;
+    const bool valid = i < whi;
+    const uint32_t d = valid ? (uint32_t)(src[i] >> shift) & 255u : 0u;
+    const uint64_t m = match_digit8(d, valid);
+    if (valid && (m & lt) == 0ull) hist[d * 16u + w] += (uint32_t)__popcll(m);
+  }
+  __syncthreads();
+  // exclusive scan over the 4096 counters; thread t owns [4t, 4t + 4)
+  uint32_t h[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h[j] = hist[4u * t + j];
+    sum += h[j];
+  }
+  uint32_t inc = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = __shfl_up(inc, d, 64);
+    if (lane >= (uint32_t)d) inc += o;
+  }
+  if (lane == 63u) s.red_a[w] = inc;
+  __syncthreads();
+  uint32_t pre = inc - sum;
+  for (uint32_t i = 0; i < w; ++i) pre += s.red_a[i];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    hist[4u * t + j] = pre;
+    pre += h[j];
+  }
+  __syncthreads();
+  for (uint32_t base = wlo; base < whi; base += 64u) {
+    const uint32_t i = base + lane;
+    const bool valid = i < whi;
+    const uint64_t e = valid ? src[i] : 0ull;
+    const uint32_t d = (uint32_t)(e >> shift) & 255u;
+    const uint64_t m = match_digit8(d, valid);
+    if (valid) {
+      const uint32_t off = hist[d * 16u + w];
+      const uint32_t r = (uint32_t)__popcll(m & lt);
+      dst[off + r] = e;
+      if (r == 0u) hist[d * 16u + w] = off + (uint32_t)__popcll(m);
+    }
+  }
+  __syncthreads();
+}
+
+// Ascending LSD radix sort of a[0..n) with tmp[0..n) as the second buffer
+// (both in LDS). Only the bits in which the keys differ are sorted, in 8-bit
+// digits starting at the lowest differing bit, so the cost is about one read
+// and one write of the list per 8 varying bits.
+__device__ __attribute__((noinline)) void radix_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n, Smem& s) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  uint64_t o = 0ull, an = ~0ull;
+  for (uint32_t j = t; j < n; j += kThreads) {
+    o |= a[j];
+    an &= a[j];
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) {
+    o |= __shfl_xor(o, d, 64);
+    an &= __shfl_xor(an, d, 64);
+  }
+  uint64_t* red = reinterpret_cast<uint64_t*>(s.wsum);
+  if (lane == 0u) red[w] = o;
+  __syncthreads();
+  uint64_t ro = 0ull;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) ro |= red[i];
+  __syncthreads();
+  if (lane == 0u) red[w] = an;
+  __syncthreads();
+  uint64_t ra = ~0ull;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) ra &= red[i];
+  __syncthreads();
+  uint64_t diff = ro ^ ra;
+  uint64_t* src = a;
+  uint64_t* dst = tmp;
+  while (diff) {
+    const uint32_t shift = (uint32_t)(__ffsll((long long)diff) - 1);
+    radix_pass(src, dst, n, shift, s);
+    uint64_t* x = src;
+    src = dst;
+    dst = x;
+    diff = shift >= 56u ? 0ull : (diff & ~((1ull << (shift + 8u)) - 1ull));
+  }
+  if (src != a) {
+    for (uint32_t j = t; j < n; j += kThreads) a[j] = src[j];
+    __syncthreads();
+  }
+}
+
 // Ascending sort of a[0..n) in LDS (keys unique or order among equal keys
 // irrelevant). n <= 256: every key counts the keys below it and is written
 // to its rank (one pass, two barriers). Larger n: bitonic network, one LDS
-// barrier per stage.
-__device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n) {
+// barrier per cross-wave stage.
+__device__ __forceinline__ void sort_u64_bitonic(uint64_t* a, uint32_t n) {
   const uint32_t t = threadIdx.x;
   if (n <= 256u) {
     uint64_t mine = 0;
@@ -396,6 +516,118 @@ __device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n) {
   __syncthreads();
 }
 
+constexpr uint32_t kBucketMax = 256;  // largest bucket ranked by direct counting
+
+// Ascending sort of a[0..n) (LDS) through tmp[0..n) (LDS). The keys are
+// spread over 4096 buckets by the 12 highest bits in which they differ
+// (bucket order is key order); every key then counts the keys of its own
+// bucket that sort before it, which gives its final position whatever
+// order the atomic scatter left inside the bucket. When a bucket holds
+// more than kBucketMax keys the radix sort takes over.
+__device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n,
+                                                          Smem& s) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  uint64_t o = 0ull, an = ~0ull;
+  for (uint32_t j = t; j < n; j += kThreads) {
+    o |= a[j];
+    an &= a[j];
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) {
+    o |= __shfl_xor(o, d, 64);
+    an &= __shfl_xor(an, d, 64);
+  }
+  uint64_t* red = reinterpret_cast<uint64_t*>(s.wsum);
+  if (lane == 0u) red[w] = o;
+  __syncthreads();
+  uint64_t ro = 0ull;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) ro |= red[i];
+  __syncthreads();
+  if (lane == 0u) red[w] = an;
+  __syncthreads();
+  uint64_t ra = ~0ull;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) ra &= red[i];
+  __syncthreads();
+  const uint64_t diff = ro ^ ra;  // bits that differ between some keys
+  if (!diff) return;              // all keys equal
+  const uint32_t hb = 63u - (uint32_t)__clzll((long long)diff);
+  const uint32_t sh = hb >= 11u ? hb - 11u : 0u;
+  uint32_t* H = s.H;
+  for (uint32_t i = t; i < 4096u; i += kThreads) H[i] = 0u;
+  __syncthreads();
+  for (uint32_t j = t; j < n; j += kThreads) atomicAdd(&H[(uint32_t)(a[j] >> sh) & 4095u], 1u);
+  __syncthreads();
+  // exclusive scan of the bucket counts (thread t owns [4t, 4t + 4)) and
+  // the largest bucket
+  uint32_t h[4], sum = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    h[j] = H[4u * t + j];
+    sum += h[j];
+    mx = max(mx, h[j]);
+  }
+  uint32_t inc = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t v = __shfl_up(inc, d, 64);
+    if (lane >= (uint32_t)d) inc += v;
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, d, 64));
+  if (lane == 63u) {
+    s.red_a[w] = inc;
+    s.red_b[w] = mx;
+  }
+  __syncthreads();
+  uint32_t pre = inc - sum, bmax = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < (uint32_t)kWaves; ++i) {
+    pre += i < w ? s.red_a[i] : 0u;
+    bmax = max(bmax, s.red_b[i]);
+  }
+  if (bmax > kBucketMax) {
+    __syncthreads();
+    radix_sort_u64(a, tmp, n, s);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    H[4u * t + j] = pre;
+    pre += h[j];
+  }
+  __syncthreads();
+  for (uint32_t j = t; j < n; j += kThreads) {
+    const uint64_t e = a[j];
+    tmp[atomicAdd(&H[(uint32_t)(e >> sh) & 4095u], 1u)] = e;
+  }
+  __syncthreads();
+  // H[b] is now the end of bucket b
+  for (uint32_t i = t; i < n; i += kThreads) {
+    const uint64_t e = tmp[i];
+    const uint32_t bk = (uint32_t)(e >> sh) & 4095u;
+    const uint32_t lo = bk ? H[bk - 1u] : 0u, hi = H[bk];
+    uint32_t r = 0;
+    for (uint32_t k = lo; k < hi; ++k) {
+      const uint64_t q = tmp[k];
+      r += (q < e || (q == e && k < i)) ? 1u : 0u;
+    }
+    a[lo + r] = e;
+  }
+  __syncthreads();
+}
+
+// Ascending sort of a[0..n) in LDS. With a free second buffer `tmp` (n
+// entries) lists above 256 entries take the bucket sort.
+__device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n, uint64_t* tmp, Smem& s) {
+  if (n > 256u && tmp) {
+    bucket_sort_u64(a, tmp, n, s);
+    return;
+  }
+  sort_u64_bitonic(a, n);
+}
+
 // Wave-aggregated append into an LDS list; returns nothing, counts all.
 __device__ __forceinline__ void list_push(uint64_t* list, uint32_t* cnt, bool p, uint64_t val) {
   unsigned long long m = __ballot(p);
@@ -429,7 +661,8 @@ __device__ __forceinline__ EcssResult row_ecss(const Row& r, X&& xf, int mode, f
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < V) ? xf(i + j, v[j]) : 0.f;
     }
-    EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum);
+    EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum,
+                                      (int)min((uint32_t)kThreads, ((V - base) + (uint32_t)M - 1u) / (uint32_t)M));
     if (e.found) {
       e.pos += (int)base;
       return e;
@@ -451,7 +684,7 @@ __device__ __forceinline__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, 
   float x[M];
 #pragma unroll
   for (int q = 0; q < M; ++q) x[q] = (j0 + q < n) ? xf(j0 + q) : 0.f;
-  return ecss_fast_chunk<M>(c0, x, mode, theta, s.ecss, s.est, s.wsum);
+  return ecss_fast_chunk<M>(c0, x, mode, theta, s.ecss, s.est, s.wsum, (int)min((uint32_t)kThreads, (n + (uint32_t)M - 1u) / (uint32_t)M));
 }
 
 template <class X>
@@ -502,7 +735,8 @@ __device__ __forceinline__ EcssResult const_ecss(uint32_t V, float u, int mode, 
     float x[M];
 #pragma unroll
     for (int j = 0; j < M; ++j) x[j] = (i0 + j < V) ? u : 0.f;
-    EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum);
+    EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum,
+                                      (int)min((uint32_t)kThreads, ((V - base) + (uint32_t)M - 1u) / (uint32_t)M));
     if (e.found) {
       e.pos += (int)base;
       return e;
@@ -567,7 +801,7 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
 
 // Final stage over the LDS list A (entries (idx << 32) | key, ascending idx,
 // n entries, every entry alive). Applies min-p, temperature, softmax, draw.
-__device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const RowParams& P, uint32_t n, float r,
+__device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a, const RowParams P, uint32_t n, float r,
                                   Smem& s, RowTrace& tr) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
@@ -622,12 +856,12 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
   EcssResult S = list_ecss(n, [&](uint32_t j) { return expf_glibc(__fsub_rn(wv(j), m3)); },
                            kEcssSum, 0.f, 0.f, s);
   const float S3 = S.c;
-  LUMEN_TICK("fin_S3", 0);
+  LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", 0);
   tr.final_sum = S3;
   EcssResult e = list_ecss(
       n, [&](uint32_t j) { return __fdiv_rn(expf_glibc(__fsub_rn(wv(j), m3)), S3); },
       kEcssFindGt, r, 0.f, s);
-  LUMEN_TICK(s.est.fail ? "walk_failed" : "walk_ok", 0);
+  LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", 0);
   LUMEN_TICK("fin_walk", 0);
   tr.cdf_before = e.found ? e.before : e.c;
   tr.cdf_at = e.c;
@@ -686,7 +920,7 @@ __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const Row
         s.Bk[j] = ((uint64_t)(~__float_as_uint(p)) << 32) | j;
       }
       __syncthreads();
-      sort_u64_asc(s.Bk, n);
+      sort_u64_asc(s.Bk, n, 2u * n <= (uint32_t)kCap ? s.Bk + n : nullptr, s);
       EcssResult w = list_ecss(
           n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); },
           kEcssFindGe, P.top_p, 0.f, s);
@@ -840,7 +1074,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
           __syncthreads();
           tr.passes++;
           const uint32_t n = s.cnt;
-          sort_u64_asc(s.A, n);  // descending key
+          sort_u64_asc(s.A, n, s.Bk, s);  // descending key
           const uint32_t cut = ~(uint32_t)(s.A[k - 1] >> 32);
           // survivors: every entry with key >= cut is a prefix of the list
           uint32_t ns = 0;
@@ -851,7 +1085,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
             s.A[j] = ((uint64_t)(uint32_t)e << 32) | (uint64_t)(~(uint32_t)(e >> 32));
           }
           __syncthreads();
-          sort_u64_asc(s.A, ns);  // ascending index
+          sort_u64_asc(s.A, ns, s.Bk, s);  // ascending index
           nlist = ns;
           small = true;
           tr.topk_cutoff_key = cut;
@@ -1011,7 +1245,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
           break;
         }
         tr.windows++;
-        sort_u64_asc(s.Bk, n);
+        sort_u64_asc(s.Bk, n, s.A, s);
         EcssResult w = list_ecss(
             n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); },
             kEcssFindGe, P.top_p, c, s);
@@ -1029,7 +1263,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
               s.A[j] = ((uint64_t)idx << 32) | tkey(v1f(row.at(idx)));
             }
             __syncthreads();
-            sort_u64_asc(s.A, nk);
+            sort_u64_asc(s.A, nk, s.Bk, s);
             nlist = nk;
             small = true;
           } else {
@@ -1413,7 +1647,7 @@ __device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b,
   LUMEN_TICK("topk_sort1", b);
   for (uint32_t j = threadIdx.x; j < ns; j += kThreads) s.A[j] = s.Bk[j];
   __syncthreads();
-  sort_u64_asc(s.A, ns);  // ascending index
+  sort_u64_asc(s.A, ns, s.Bk, s);  // ascending index
   tr.topk_cutoff_key = cut;
   tr.topk_survivors = ns;
   LUMEN_TICK("topk_sorted", b);
@@ -1503,7 +1737,8 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
     // rounding drift of a long f32 sum is typically ~1e-5 relative. A wrong
     // guess only costs the exact recomputation in chain_walk.
     EstThread et;
-    if (est_prepare<M>(x, pt, d, 4e-5, s.ecss, s.est, et)) {
+    if (est_prepare<M>(x, pt, d, 4e-5, s.ecss, s.est, et,
+                       (int)min((uint32_t)kThreads, ((sc.hi - (sc.lo + q * chunk)) + (uint32_t)M - 1u) / (uint32_t)M))) {
       fits |= 1u << q;
       copy_words(est_slot(a, b, sl, q), reinterpret_cast<const uint32_t*>(&s.est), nw);
     }
@@ -1542,14 +1777,21 @@ __device__ __forceinline__ float chain_walk_slice(const KernelArgs& a, int b, ui
         done = true;
       }
     }
+    LUMEN_TICK(done ? "walk_fast" : "walk_miss", b);
     if (!done) {
       float x[M];
       chain_load<M>(row, sc, sc.lo + q * chunk + (uint32_t)threadIdx.x * M, m1, x);
       c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
+      LUMEN_TICK("walk_recomputed", b);
     }
   }
   return c;
 }
+
+__device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b, const RowParams P,
+                                                     const Row row, float m1, float S1, uint32_t tau,
+                                                     uint32_t ncand, const uint64_t* cand,
+                                                     float rdraw, Smem& s, RowTrace tr);
 
 // Top-p without top-k or penalties. Pass 1 (all slices): slice max, an
 // exp-sum estimate, and the candidates above a sampled logit threshold.
@@ -1643,6 +1885,7 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
     }
     __syncthreads();
   }
+  LUMEN_TICK("p_prefetched", b);
   float S1 = 0.f;
   for (uint32_t i = 0; i < G; ++i) {
     const Slice si = slice_bounds(V, G, i);
@@ -1656,7 +1899,18 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
   tr.path = 4u;
   tr.passes = 2;
   tr.topp_sum = S1;
-  // window 1: candidates with p >= p(tau)
+  topp_window(a, b, P, row, m1, S1, tau, ncand, cand, rdraw, s, tr);
+}
+
+// Window 1 of the top-p order: the candidates with p >= p(tau), sorted by
+// (p desc, index asc), walked with the exact cumulative sum; the kept prefix
+// continues on the small path in index order. A crossing outside the window
+// hands the row to the exact single-workgroup path.
+__device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b, const RowParams P,
+                                                     const Row row, float m1, float S1, uint32_t tau,
+                                                     uint32_t ncand, const uint64_t* cand,
+                                                     float rdraw, Smem& s, RowTrace tr) {
+  const float tv = tau ? key2f(tau) : kNegInf;
   const float p_lo = tau ? __fdiv_rn(expf_glibc(__fsub_rn(tv, m1)), S1) : 0.f;
   if (threadIdx.x == 0) s.cnt = 0;
   __syncthreads();
@@ -1676,12 +1930,12 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
   __syncthreads();
   const uint32_t n = s.cnt;
   LUMEN_TICK("p_window_built", b);
-  sort_u64_asc(s.Bk, n);
+  sort_u64_asc(s.Bk, n, s.A, s);
   LUMEN_TICK("p_window_sorted", b);
   EcssResult wk = list_ecss(
       n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe,
       P.top_p, 0.f, s);
-  LUMEN_TICK("p_walked", b);
+  LUMEN_TICK(s.est.fail == 2 ? "p_walk_nofit" : s.est.fail ? "p_walk_failed" : "p_walk_ok", b);
   if (!wk.found) {
     row_single(a, b, s);
     return;
@@ -1695,7 +1949,7 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
     s.A[j] = ((uint64_t)idx << 32) | tkey(row.at(idx));
   }
   __syncthreads();
-  sort_u64_asc(s.A, nk);
+  sort_u64_asc(s.A, nk, s.Bk, s);
   LUMEN_TICK("p_kept_sorted", b);
   small_path(a, b, P, nk, true, rdraw, s, tr);
 }
