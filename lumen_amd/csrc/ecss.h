@@ -31,6 +31,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "wave.h"
+
 namespace lumen {
 
 constexpr int kThreads = 1024;
@@ -78,38 +80,17 @@ __device__ __forceinline__ bool ecss_cond(int mode, float c, float theta) {
 // Exclusive block scan of parity maps (identity = {0,0}).
 __device__ __forceinline__ PMap block_excl_scan(PMap v, EcssShared& sh) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  PMap inc = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    PMap L;
-    L.a0 = __shfl_up(inc.a0, d, 64);
-    L.a1 = __shfl_up(inc.a1, d, 64);
-    if (lane >= d) inc = pm_combine(L, inc);
-  }
+  const PMap id{0u, 0u};
+  const PMap inc = wave_scan_incl(v, id, pm_combine);
   if (lane == 63) sh.wave_tot[w] = inc;
   __syncthreads();
   if (w == 0) {
-    PMap t = (lane < kWaves) ? sh.wave_tot[lane] : PMap{0u, 0u};
-    PMap ti = t;
-#pragma unroll
-    for (int d = 1; d < kWaves; d <<= 1) {
-      PMap L;
-      L.a0 = __shfl_up(ti.a0, d, 64);
-      L.a1 = __shfl_up(ti.a1, d, 64);
-      if (lane >= d) ti = pm_combine(L, ti);
-    }
-    PMap ex;
-    ex.a0 = __shfl_up(ti.a0, 1, 64);
-    ex.a1 = __shfl_up(ti.a1, 1, 64);
-    if (lane == 0) ex = PMap{0u, 0u};
+    const PMap t = (lane < kWaves) ? sh.wave_tot[lane] : id;
+    const PMap ex = wave_shr1(wave_scan_incl(t, id, pm_combine), id);
     if (lane < kWaves) sh.wave_pre[lane] = ex;
   }
   __syncthreads();
-  PMap ex;
-  ex.a0 = __shfl_up(inc.a0, 1, 64);
-  ex.a1 = __shfl_up(inc.a1, 1, 64);
-  if (lane == 0) ex = PMap{0u, 0u};
-  return pm_combine(sh.wave_pre[w], ex);
+  return pm_combine(sh.wave_pre[w], wave_shr1(inc, id));
 }
 
 // One chunk: thread t holds x[0..M) = chunk elements t*M .. t*M+M-1, all
@@ -293,25 +274,13 @@ __device__ __forceinline__ uint32_t est_binade(double x) {
   return __float_as_uint(f) & 0xff800000u;
 }
 
-__device__ __forceinline__ SegVal shfl_up_seg(SegVal v, int d) {
-  SegVal o;
-  o.head = __shfl_up(v.head, d, 64);
-  o.m.a0 = __shfl_up(v.m.a0, d, 64);
-  o.m.a1 = __shfl_up(v.m.a1, d, 64);
-  return o;
-}
-
 // Inclusive segmented block scan; *prev receives the inclusive value of the
 // previous thread (identity for thread 0).
 __device__ __forceinline__ SegVal seg_scan_incl(SegVal v, EcssShared& sh, EstShared& es,
                                                 SegVal* prev) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  SegVal inc = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    SegVal L = shfl_up_seg(inc, d);
-    if (lane >= d) inc = seg_combine(L, inc);
-  }
+  const SegVal id{0u, PMap{0u, 0u}};
+  const SegVal inc = wave_scan_incl(v, id, seg_combine);
   if (lane == 63) {
     sh.wave_tot[w] = inc.m;
     es.wave_head[w] = inc.head;
@@ -321,13 +290,7 @@ __device__ __forceinline__ SegVal seg_scan_incl(SegVal v, EcssShared& sh, EstSha
     SegVal t;
     t.head = lane < kWaves ? es.wave_head[lane] : 0u;
     t.m = lane < kWaves ? sh.wave_tot[lane] : PMap{0u, 0u};
-#pragma unroll
-    for (int d = 1; d < kWaves; d <<= 1) {
-      SegVal L = shfl_up_seg(t, d);
-      if (lane >= d) t = seg_combine(L, t);
-    }
-    SegVal ex = shfl_up_seg(t, 1);
-    if (lane == 0) ex = SegVal{0u, PMap{0u, 0u}};
+    const SegVal ex = wave_shr1(wave_scan_incl(t, id, seg_combine), id);
     if (lane < kWaves) {
       sh.wave_pre[lane] = ex.m;
       es.wave_head[kWaves + lane] = ex.head;
@@ -337,9 +300,9 @@ __device__ __forceinline__ SegVal seg_scan_incl(SegVal v, EcssShared& sh, EstSha
   SegVal pre;
   pre.head = es.wave_head[kWaves + w];
   pre.m = sh.wave_pre[w];
-  SegVal in_w = shfl_up_seg(inc, 1);
-  SegVal r = seg_combine(pre, inc);
-  *prev = (lane == 0) ? pre : seg_combine(pre, in_w);
+  const SegVal in_w = wave_shr1(inc, id);
+  const SegVal r = seg_combine(pre, inc);
+  *prev = seg_combine(pre, in_w);
   __syncthreads();
   return r;
 }
@@ -400,7 +363,7 @@ __device__ __forceinline__ bool est_prepare(const float (&x)[M], double p_start,
   const bool fits = nb <= kEstMaxB && nb * M <= kEstBx;
   if (fits) {
     // predecessor's boundary flag and binade
-    uint32_t pb = __shfl_up(et.boundary, 1, 64), pbin = __shfl_up(et.bin, 1, 64);
+    uint32_t pb = wave_shr1(et.boundary, 0u), pbin = wave_shr1(et.bin, 0u);
     if (lane == 0 && w > 0) {
       pb = es.wave_lastb[w - 1];
       pbin = es.wave_lastbin[w - 1];
@@ -550,16 +513,12 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
 #pragma unroll
   for (int j = 0; j < M; ++j) d += (double)x[j];
   // exclusive f64 block scan of d
-  double inc = d;
-#pragma unroll
-  for (int k = 1; k < 64; k <<= 1) {
-    double o = __shfl_up(inc, k, 64);
-    if (lane >= k) inc += o;
-  }
+  const double inc = wave_scan_incl(d, 0.0, [](double l, double r) { return l + r; });
   if (lane == 63) wsum[w] = inc;
   __syncthreads();
   double pre = 0.0;
-  for (int i = 0; i < w; ++i) pre += wsum[i];
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) pre += i < w ? wsum[i] : 0.0;
   __syncthreads();
   const double p_start = (double)c + pre + inc - d;
   const double rel = (double)((t + 1) * M) * 0x1.0p-24 * 1.01 + 1e-9;

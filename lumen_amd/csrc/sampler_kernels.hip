@@ -40,12 +40,12 @@
 // once when that row's result is written.
 #ifdef LUMEN_TIMING
 #include <cstdio>
-__shared__ unsigned long long g_ticks[48];
-__shared__ const char* g_tick_names[48];
+__shared__ unsigned long long g_ticks[40];
+__shared__ const char* g_tick_names[40];
 __shared__ int g_nticks;
 #define LUMEN_TICK(label, b)                                         \
   do {                                                              \
-    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 48) {            \
+    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 40) {            \
       g_ticks[g_nticks] = wall_clock64();                           \
       g_tick_names[g_nticks++] = label;                             \
     }                                                               \
@@ -70,6 +70,7 @@ __shared__ int g_nticks;
 namespace lumen {
 
 constexpr int kCap = 8192;          // LDS list capacity (entries)
+constexpr int kSlots = kMaxSlices * kChainMaxQ;  // parked run records per row
 constexpr int kCapWindow = kCap - 512;  // planned window size (margin for equal-probability spill)
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -87,6 +88,8 @@ struct Smem {
   uint32_t cnt;
   int misc_i[4];
   uint32_t misc_u[4];
+  uint32_t misc_slot[2 * kSlots];  // chained-sum record offsets and slot ids
+  uint32_t misc_size[kSlots];
 };
 
 // ---------------------------------------------------------------- helpers
@@ -179,11 +182,11 @@ __device__ __forceinline__ void range_foreach(const Row& r, uint32_t lo, uint32_
   }
 }
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ uint32_t op_add_u32(uint32_t l, uint32_t r) { return l + r; }
+__device__ __forceinline__ uint32_t op_or_u32(uint32_t l, uint32_t r) { return l | r; }
+__device__ __forceinline__ uint64_t op_max_u64(uint64_t l, uint64_t r) { return l > r ? l : r; }
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return wave_reduce(v, 0u, op_add_u32); }
 
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -199,8 +202,7 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
 
 __device__ __forceinline__ uint32_t block_or_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+  v = wave_reduce(v, 0u, op_or_u32);
   if (lane == 0) s.red_a[w] = v;
   __syncthreads();
   uint32_t r = 0;
@@ -213,13 +215,7 @@ __device__ __forceinline__ uint32_t block_or_u32(uint32_t v, Smem& s) {
 // max of a 64-bit value carried as (hi, lo)
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
-    uint32_t lo = __shfl_xor((uint32_t)v, o, 64);
-    uint64_t u = ((uint64_t)hi << 32) | lo;
-    v = u > v ? u : v;
-  }
+  v = wave_reduce(v, (uint64_t)0, op_max_u64);
   if (lane == 0) {
     s.red_a[w] = (uint32_t)(v >> 32);
     s.red_b[w] = (uint32_t)v;
@@ -238,8 +234,7 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Smem& s) {
 // fold(-inf, f32::max) over the block; NaN inputs are ignored
 __device__ __forceinline__ float block_rmax(float v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = rmax(v, __shfl_xor(v, o, 64));
+  v = wave_reduce(v, kNegInf, rmax);
   if (lane == 0) s.red_f[w] = v;
   __syncthreads();
   float r = kNegInf;
@@ -251,15 +246,12 @@ __device__ __forceinline__ float block_rmax(float v, Smem& s) {
 
 __device__ __forceinline__ uint32_t block_incl_scan_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    uint32_t o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+  v = wave_scan_incl(v, 0u, op_add_u32);
   if (lane == 63) s.red_a[w] = v;
   __syncthreads();
   uint32_t pre = 0;
-  for (int i = 0; i < w; ++i) pre += s.red_a[i];
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) pre += i < w ? s.red_a[i] : 0u;
   __syncthreads();
   return v + pre;
 }
@@ -368,12 +360,7 @@ __device__ __forceinline__ void radix_pass(const uint64_t* src, uint64_t* dst, u
     h[j] = hist[4u * t + j];
     sum += h[j];
   }
-  uint32_t inc = sum;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t o = __shfl_up(inc, d, 64);
-    if (lane >= (uint32_t)d) inc += o;
-  }
+  const uint32_t inc = wave_scan_incl(sum, 0u, op_add_u32);
   if (lane == 63u) s.red_a[w] = inc;
   __syncthreads();
   uint32_t pre = inc - sum;
@@ -411,11 +398,8 @@ __device__ __attribute__((noinline)) void radix_sort_u64(uint64_t* a, uint64_t* 
     o |= a[j];
     an &= a[j];
   }
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) {
-    o |= __shfl_xor(o, d, 64);
-    an &= __shfl_xor(an, d, 64);
-  }
+  o = wave_reduce(o, (uint64_t)0, [](uint64_t l, uint64_t r) { return l | r; });
+  an = wave_reduce(an, ~(uint64_t)0, [](uint64_t l, uint64_t r) { return l & r; });
   uint64_t* red = reinterpret_cast<uint64_t*>(s.wsum);
   if (lane == 0u) red[w] = o;
   __syncthreads();
@@ -532,11 +516,8 @@ __device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t*
     o |= a[j];
     an &= a[j];
   }
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) {
-    o |= __shfl_xor(o, d, 64);
-    an &= __shfl_xor(an, d, 64);
-  }
+  o = wave_reduce(o, (uint64_t)0, [](uint64_t l, uint64_t r) { return l | r; });
+  an = wave_reduce(an, ~(uint64_t)0, [](uint64_t l, uint64_t r) { return l & r; });
   uint64_t* red = reinterpret_cast<uint64_t*>(s.wsum);
   if (lane == 0u) red[w] = o;
   __syncthreads();
@@ -568,14 +549,8 @@ __device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t*
     sum += h[j];
     mx = max(mx, h[j]);
   }
-  uint32_t inc = sum;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t v = __shfl_up(inc, d, 64);
-    if (lane >= (uint32_t)d) inc += v;
-  }
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, d, 64));
+  const uint32_t inc = wave_scan_incl(sum, 0u, op_add_u32);
+  mx = wave_reduce(mx, 0u, [](uint32_t l, uint32_t r) { return l > r ? l : r; });
   if (lane == 63u) {
     s.red_a[w] = inc;
     s.red_b[w] = mx;
@@ -636,7 +611,7 @@ __device__ __forceinline__ void list_push(uint64_t* list, uint32_t* cnt, bool p,
   uint32_t base = 0;
   int leader = __ffsll((long long)m) - 1;
   if (lane == leader) base = atomicAdd(cnt, (uint32_t)__popcll(m));
-  base = __shfl(base, leader, 64);
+  base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);
   if (p) {
     uint32_t off = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
     if (off < (uint32_t)kCap) list[off] = val;
@@ -1426,23 +1401,6 @@ __device__ __forceinline__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem
   return ok;
 }
 
-// Wave-aggregated append of `val` to a row's global candidate buffer.
-__device__ __forceinline__ void cand_push(uint64_t* cand, uint32_t* cnt, bool p, uint64_t val) {
-  unsigned long long m = __ballot(p);
-  if (!m) return;
-  const int lane = threadIdx.x & 63;
-  const int leader = __ffsll((long long)m) - 1;
-  uint32_t base = 0;
-  if (lane == leader)
-    base = __hip_atomic_fetch_add(cnt, (uint32_t)__popcll(m), __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-  base = __shfl(base, leader, 64);
-  if (p) {
-    uint32_t off = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-    if (off < (uint32_t)kCandCap) cand[off] = val;
-  }
-}
-
 // Appends this workgroup's candidates, gathered in s.A[0..s.cnt) by
 // list_push, to the row's global buffer with a single atomic. The count is
 // always added in full, so an overflow (of LDS or of the buffer) shows up as
@@ -1512,9 +1470,21 @@ __device__ __forceinline__ void slice_pen_out(const KernelArgs& a, int b, const 
   }
 }
 
+// Per-row values every path needs, derived from the arguments inside each
+// path function (so the kernel entry passes only scalars to it).
+#define ROW_CONTEXT(a, b)                                                             \
+  const RowParams P = (a).inline_rows ? (a).inline_params[b] : (a).params[b];         \
+  const float rdraw = (a).inline_draws ? (a).inline_uniforms[b] : (a).uniforms[b];    \
+  RowWs& ws = (a).ws[b];                                                              \
+  uint64_t* cand = (a).cand + (uint64_t)(b) * kCandCap;                               \
+  const Row row = make_row((a), (b));                                                 \
+  (void)rdraw;                                                                        \
+  (void)cand
+
 // Greedy: per-slice argmax, the last workgroup to arrive combines.
-__device__ __attribute__((noinline)) void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
-                             const RowParams& P, const Row& row, RowWs& ws, Smem& s) {
+__device__ __forceinline__ void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                                                      Smem& s) {
+  ROW_CONTEXT(a, b);
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
   const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
@@ -1557,9 +1527,9 @@ __device__ __attribute__((noinline)) void greedy_split(const KernelArgs& a, int 
 // candidate buffer, and the last workgroup finishes on the LDS list. If the
 // sample missed (fewer than k or more than the buffer holds), the finisher
 // runs the exact single-workgroup path.
-__device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
-                           const RowParams& P, const Row& row, RowWs& ws, uint64_t* cand,
-                           float rdraw, Smem& s) {
+__device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                                                    Smem& s) {
+  ROW_CONTEXT(a, b);
   const uint32_t V = a.vocab;
   const uint32_t k = P.top_k;
   const Slice sc = slice_bounds(V, G, sl);
@@ -1657,12 +1627,7 @@ __device__ __attribute__((noinline)) void topk_split(const KernelArgs& a, int b,
 
 __device__ __forceinline__ double block_excl_scan_f64(double v, Smem& s, double* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  double inc = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    double o = __shfl_up(inc, d, 64);
-    if (lane >= d) inc += o;
-  }
+  const double inc = wave_scan_incl(v, 0.0, [](double l, double r) { return l + r; });
   __shared__ double wt[kWaves];
   if (lane == 63) wt[w] = inc;
   __syncthreads();
@@ -1710,8 +1675,27 @@ __device__ __forceinline__ uint32_t* est_slot(const KernelArgs& a, int b, uint32
   return a.est + (((uint64_t)b * kMaxSlices + sl) * kChainMaxQ + q) * (kEstSharedBytes / 4);
 }
 
-__device__ __forceinline__ void copy_words(uint32_t* dst, const uint32_t* src, uint32_t nw) {
-  for (uint32_t i = threadIdx.x; i < nw; i += kThreads) dst[i] = src[i];
+
+// A run structure is parked as a compact record of 32-bit words:
+//   [0]                    nb (boundary threads)
+//   [1 + 3k .. 3 + 3k]     run k (k = 0..nb): binade bits, map a0, map a1
+//   [4 + 3nb ..]           the M summands of every boundary thread, in order
+template <int M>
+__device__ __forceinline__ uint32_t record_words(uint32_t nb) {
+  return 1u + 3u * (nb + 1u) + nb * (uint32_t)M;
+}
+
+template <int M>
+__device__ __forceinline__ void park_record(uint32_t* dst, const EstShared& es) {
+  const uint32_t t = threadIdx.x, nb = (uint32_t)es.nb;
+  if (t == 0) dst[0] = nb;
+  if (t <= nb) {
+    dst[1u + 3u * t] = es.seg_bin[t];
+    dst[2u + 3u * t] = es.seg_tot[t].a0;
+    dst[3u + 3u * t] = es.seg_tot[t].a1;
+  }
+  const uint32_t* bx = reinterpret_cast<const uint32_t*>(es.bx);
+  for (uint32_t i = t; i < nb * (uint32_t)M; i += kThreads) dst[4u + 3u * nb + i] = bx[i];
 }
 
 template <int M>
@@ -1720,7 +1704,6 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
                                                   double p_slice, Smem& s) {
   const uint32_t chunk = (uint32_t)kThreads * M;
   const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;
-  const uint32_t nw = (uint32_t)((sizeof(EstShared) + 3) / 4);
   uint32_t fits = 0;
   double pre = p_slice;
   for (uint32_t q = 0; q < nq; ++q) {
@@ -1740,50 +1723,111 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
     if (est_prepare<M>(x, pt, d, 4e-5, s.ecss, s.est, et,
                        (int)min((uint32_t)kThreads, ((sc.hi - (sc.lo + q * chunk)) + (uint32_t)M - 1u) / (uint32_t)M))) {
       fits |= 1u << q;
-      copy_words(est_slot(a, b, sl, q), reinterpret_cast<const uint32_t*>(&s.est), nw);
+      park_record<M>(est_slot(a, b, sl, q), s.est);
     }
     __syncthreads();
   }
   return fits;
 }
 
-// Number of EstShared structures that fit in the LDS list area (A and Bk).
-constexpr uint32_t kParkedInLds = (uint32_t)(2u * kCap * sizeof(uint64_t) / sizeof(EstShared));
-
+// Exact softmax sum of the row from the parked records (last workgroup of
+// the row). The records of all slots (slice i, sub-chunk q, in row order)
+// are gathered into the list area with one bulk copy; thread 0 then walks
+// runs and boundary summands in order. A slot without a record, or whose
+// record does not match the exact running sum (wrong binade guess), is
+// recomputed by the whole workgroup with the iterative method, and the walk
+// resumes after it.
 template <int M>
-__device__ __forceinline__ float chain_walk_slice(const KernelArgs& a, int b, uint32_t sl,
-                                                  const Row& row, Slice sc, float m1,
-                                                  uint32_t fits, float c, Smem& s) {
+__device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t G, const Row& row,
+                                           float m1, RowWs& ws, Smem& s) {
+  const uint32_t t = threadIdx.x, V = a.vocab;
   const uint32_t chunk = (uint32_t)kThreads * M;
-  const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;
-  const uint32_t nw = (uint32_t)((sizeof(EstShared) + 3) / 4);
-  for (uint32_t q = 0; q < nq; ++q) {
-    bool done = false;
-    if ((fits >> q) & 1u) {
-      // the finisher copied the first kParkedInLds parked structures into the list area
-      const uint32_t slot = sl * kChainMaxQ + q;
-      EstShared* es = slot < kParkedInLds ? reinterpret_cast<EstShared*>(s.A) + slot : &s.est;
-      if (slot >= kParkedInLds) {
-        copy_words(reinterpret_cast<uint32_t*>(&s.est), est_slot(a, b, sl, q), nw);
-        __syncthreads();
+  uint32_t* off = s.misc_slot;  // [0..kSlots]: record offsets; kSlots + j: slot id
+  uint32_t* words = reinterpret_cast<uint32_t*>(s.A);
+  // slot list, record sizes and offsets (one wave)
+  if (t < 64u) {
+    uint32_t id = 0xffffffffu, size = 0;
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < G; ++i) {
+      const Slice si = slice_bounds(V, G, i);
+      const uint32_t nq = (si.hi - si.lo + chunk - 1u) / chunk;
+      const uint32_t fi = __hip_atomic_load(&ws.part_fits[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (uint32_t q = 0; q < nq; ++q, ++n) {
+        if (n == t) {
+          id = i * kChainMaxQ + q;
+          if ((fi >> q) & 1u) size = record_words<M>(est_slot(a, b, i, q)[0]);
+        }
       }
-      float xz[M];
+    }
+    const uint32_t inc = wave_scan_incl(size, 0u, op_add_u32);
+    if (t < (uint32_t)kSlots) {
+      off[t] = inc - size;
+      off[kSlots + t] = id;
+      s.misc_size[t] = size;
+    }
+    if (t == 0) s.misc_u[3] = n;
+    if (t == 63u) s.misc_u[2] = inc;
+  }
+  __syncthreads();
+  const uint32_t nslots = s.misc_u[3];
+  const uint32_t total = s.misc_u[2];
+  for (uint32_t w = t; w < total; w += kThreads) {
+    uint32_t j = 0;
+    while (j + 1u < nslots && off[j + 1u] <= w) ++j;
+    const uint32_t id = off[kSlots + j];
+    words[w] = est_slot(a, b, id / kChainMaxQ, id % kChainMaxQ)[w - off[j]];
+  }
+  __syncthreads();
+  LUMEN_TICK("p_prefetched", b);
+  float c = 0.f;
+  uint32_t j0 = 0;
+  while (j0 < nslots) {
+    if (t == 0) {
+      float cc = c;
+      uint32_t j = j0;
+      for (; j < nslots; ++j) {
+        if (s.misc_size[j] == 0u) break;
+        const uint32_t* r = words + off[j];
+        const uint32_t nb = r[0];
+        bool ok = true;
+        float y = cc;
+        for (uint32_t k = 0; k <= nb && ok; ++k) {
+          const uint32_t sb = r[1u + 3u * k];
+          if (sb != kEmptyRun) {
+            const uint32_t cb = __float_as_uint(y);
+            const uint32_t inc = (cb & 1u) ? r[3u + 3u * k] : r[2u + 3u * k];
+            const uint32_t nbits = cb + inc;
+            if ((cb & 0xff800000u) != sb || inc >= kSat || nbits >= sb + 0x00800000u) {
+              ok = false;
+              break;
+            }
+            y = __uint_as_float(nbits);
+          }
+          if (k == nb) break;
+          const float* bx = reinterpret_cast<const float*>(r + 4u + 3u * nb) + k * (uint32_t)M;
 #pragma unroll
-      for (int j = 0; j < M; ++j) xz[j] = 0.f;
-      EstThread et{};
-      EcssResult r;
-      if (est_resolve<M>(c, xz, kEcssSum, 0.f, et, s.ecss, *es, &r)) {
-        c = r.c;
-        done = true;
+          for (int q = 0; q < M; ++q) y = __fadd_rn(y, bx[q]);
+        }
+        if (!ok) break;
+        cc = y;
       }
+      s.misc_u[0] = j;
+      s.red_f[0] = cc;
     }
-    LUMEN_TICK(done ? "walk_fast" : "walk_miss", b);
-    if (!done) {
-      float x[M];
-      chain_load<M>(row, sc, sc.lo + q * chunk + (uint32_t)threadIdx.x * M, m1, x);
-      c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
-      LUMEN_TICK("walk_recomputed", b);
-    }
+    __syncthreads();
+    const uint32_t j = s.misc_u[0];
+    c = s.red_f[0];
+    __syncthreads();
+    if (j >= nslots) break;
+    // exact recomputation of slot j
+    const uint32_t id = off[kSlots + j];
+    const Slice si = slice_bounds(V, G, id / kChainMaxQ);
+    const uint32_t lo = si.lo + (id % kChainMaxQ) * chunk;
+    float x[M];
+    chain_load<M>(row, si, lo + t * (uint32_t)M, m1, x);
+    c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
+    LUMEN_TICK("walk_recomputed", b);
+    j0 = j + 1u;
   }
   return c;
 }
@@ -1799,9 +1843,9 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
 // The last slice then walks the candidates in probability order (window 1 of
 // the reference's sorted order); if the crossing is not inside it, the exact
 // single-workgroup path takes over.
-__device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
-                           const RowParams& P, const Row& row, RowWs& ws, uint64_t* cand,
-                           float rdraw, Smem& s) {
+__device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                                                    Smem& s) {
+  ROW_CONTEXT(a, b);
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
@@ -1873,26 +1917,7 @@ __device__ __attribute__((noinline)) void topp_split(const KernelArgs& a, int b,
     row_single(a, b, s);
     return;
   }
-  {
-    // bring every parked structure of the row into LDS with one bulk copy
-    const uint32_t nw = (uint32_t)((sizeof(EstShared) + 3) / 4);
-    const uint32_t nslots = min(G * (uint32_t)kChainMaxQ, kParkedInLds);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(s.A);
-    for (uint32_t x = threadIdx.x; x < nslots * nw; x += kThreads) {
-      const uint32_t slot = x / nw, word = x - slot * nw;
-      dst[slot * (uint32_t)(sizeof(EstShared) / 4) + word] =
-          est_slot(a, b, slot / kChainMaxQ, slot % kChainMaxQ)[word];
-    }
-    __syncthreads();
-  }
-  LUMEN_TICK("p_prefetched", b);
-  float S1 = 0.f;
-  for (uint32_t i = 0; i < G; ++i) {
-    const Slice si = slice_bounds(V, G, i);
-    const uint32_t fi = __hip_atomic_load(&ws.part_fits[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    S1 = m16 ? chain_walk_slice<16>(a, b, i, row, si, m1, fi, S1, s)
-             : chain_walk_slice<32>(a, b, i, row, si, m1, fi, S1, s);
-  }
+  const float S1 = m16 ? chain_sum<16>(a, b, G, row, m1, ws, s) : chain_sum<32>(a, b, G, row, m1, ws, s);
   LUMEN_TICK("p_chain", b);
   RowTrace tr;
   init_trace(tr, V);
@@ -1910,18 +1935,79 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
                                                      const Row row, float m1, float S1, uint32_t tau,
                                                      uint32_t ncand, const uint64_t* cand,
                                                      float rdraw, Smem& s, RowTrace tr) {
+  const uint32_t t = threadIdx.x;
   const float tv = tau ? key2f(tau) : kNegInf;
-  const float p_lo = tau ? __fdiv_rn(expf_glibc(__fsub_rn(tv, m1)), S1) : 0.f;
-  if (threadIdx.x == 0) s.cnt = 0;
+  // The candidates hold every logit >= tau (and a margin below). Their
+  // exp-mass per logit bin, accumulated from the top, gives the lowest bin
+  // whose cumulative mass already exceeds top_p * S1 with a margin; window 1
+  // then only needs the candidates from that bin's lower edge up (never below
+  // tau). The bin masses only steer the window size: the crossing itself is
+  // found exactly on the sorted window, and a window that misses it hands
+  // the row to the exact path.
+  constexpr uint32_t kBins = 512;
+  float* hmass = reinterpret_cast<float*>(s.H);
+  const float span = tau ? __fsub_rn(m1, tv) : 0.f;
+  const bool binned = tau && span > 0.f;
+  const float inv_w = binned ? __fdiv_rn((float)kBins, span) : 0.f;
+  for (uint32_t i = t; i < kBins; i += kThreads) hmass[i] = 0.f;
   __syncthreads();
-  for (uint32_t base = 0; base < ncand; base += kThreads) {
-    const uint32_t j = base + threadIdx.x;
+  // stage the candidates in LDS as (exp(v - m1) bits << 32) | index, all
+  // loads in flight together; bin the exp-mass of those >= tau
+  const uint32_t nc = min(ncand, (uint32_t)kCap);
+  for (uint32_t base = 0; base < nc; base += 8u * kThreads) {
+    uint64_t c[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t j = base + (uint32_t)q * kThreads + t;
+      c[q] = j < nc ? cand[j] : 0ull;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t j = base + (uint32_t)q * kThreads + t;
+      if (j < nc) {
+        const float v = key2f(~(uint32_t)(c[q] >> 32));
+        const float x = expf_glibc(__fsub_rn(v, m1));
+        s.A[j] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)c[q];
+        if (binned && v >= tv)
+          atomicAdd(&hmass[min(kBins - 1u, (uint32_t)(__fsub_rn(m1, v) * inv_w))], x);
+      }
+    }
+  }
+  __syncthreads();
+  float v_thr = tv;
+  if (binned) {
+    // first bin (from the top) where the running mass reaches the target
+    if (t < 64u) {
+      const float target = fminf(__fmul_rn(__fmul_rn(P.top_p, S1), 1.004f), S1);
+      float run = 0.f;
+      uint32_t hit = kBins;
+      for (uint32_t base = 0; base < kBins && hit == kBins; base += 64u) {
+        const float m =
+            wave_scan_incl(hmass[base + t], 0.f, [](float l, float r) { return l + r; });
+        const unsigned long long hm = __ballot(run + m >= target);
+        if (hm) hit = base + (uint32_t)(__ffsll((long long)hm) - 1);
+        run += wave_read(m, 63);
+      }
+      if (t == 0) s.misc_u[2] = hit;
+    }
+    __syncthreads();
+    const uint32_t hit = s.misc_u[2];
+    if (hit + 2u < kBins) {
+      // one spare bin below: binning rounds (m1 - v) / w
+      const float edge = __fsub_rn(m1, __fmul_rn((float)(hit + 2u), __fdiv_rn(span, (float)kBins)));
+      v_thr = fmaxf(tv, edge);
+    }
+  }
+  const float p_lo = tau ? __fdiv_rn(expf_glibc(__fsub_rn(v_thr, m1)), S1) : 0.f;
+  if (t == 0) s.cnt = 0;
+  __syncthreads();
+  for (uint32_t base = 0; base < nc; base += kThreads) {
+    const uint32_t j = base + t;
     bool in = false;
     uint64_t e = 0;
-    if (j < ncand) {
-      const uint64_t c = cand[j];
-      const float v = key2f(~(uint32_t)(c >> 32));
-      const float p = __fdiv_rn(expf_glibc(__fsub_rn(v, m1)), S1);
+    if (j < nc) {
+      const uint64_t c = s.A[j];
+      const float p = __fdiv_rn(__uint_as_float((uint32_t)(c >> 32)), S1);
       in = p > 0.f && p >= p_lo;
       e = ((uint64_t)(~__float_as_uint(p)) << 32) | (uint32_t)c;
     }
@@ -1954,6 +2040,42 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
   small_path(a, b, P, nk, true, rdraw, s, tr);
 }
 
+// Row and slice of this workgroup. With xcd_rows, blocks are dispatched to
+// the 8 XCDs round-robin: a row's slices stay on one XCD so its
+// coordination traffic stays in that XCD's L2.
+__device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint32_t& sl) {
+  const uint32_t G = a.slices;
+  if (a.xcd_rows) {
+    const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
+    b = xcd + 8u * (j / G);
+    sl = j % G;
+  } else {
+    b = blockIdx.x / G;
+    sl = blockIdx.x % G;
+  }
+}
+
+// The last workgroup of a row to leave restores its coordination block. The
+// row is derived again from the block index, so nothing has to stay live
+// across the path calls.
+__device__ __attribute__((noinline)) void row_exit(const KernelArgs& a, Smem& s) {
+  uint32_t b, sl;
+  block_row(a, b, sl);
+  const uint32_t G = a.slices;
+  RowWs& ws = a.ws[b];
+  const uint32_t old = wg_arrive(&ws.exit_, s);
+  if (old == G - 1u && threadIdx.x == 0) {
+    ws.arrive = 0;
+    ws.bar = 0;
+    ws.cand_n = 0;
+    ws.status = 0;
+    for (uint32_t i = 0; i < G; ++i) ws.chain_flag[i] = 0;
+    __threadfence();
+    ws.exit_ = 0;
+    __threadfence();
+  }
+}
+
 extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs args) {
   // Device functions receive the arguments by reference. Referencing the
   // by-value parameter would make every thread copy it to private memory;
@@ -1966,62 +2088,28 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
   LUMEN_TICK_INIT();
   const uint32_t G = a.slices;
   uint32_t b, sl;
-  if (a.xcd_rows) {
-    // blocks are dispatched to the 8 XCDs round-robin: keep a row's slices on
-    // one XCD so its coordination traffic stays in that XCD's L2
-    const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
-    b = xcd + 8u * (j / G);
-    sl = j % G;
-  } else {
-    b = blockIdx.x / G;
-    sl = blockIdx.x % G;
-  }
+  block_row(a, b, sl);
   if (b >= a.batch) return;
-#ifdef LUMEN_GREEDY_ONLY
-  {
-    const Row row = make_row(a, (int)b);
-    const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
-    uint64_t best = 0;
-    row_foreach(row, [&](uint32_t i, float v) {
-      uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
-      best = k > best ? k : best;
-    });
-    best = block_max_u64(best, s);
-    if (threadIdx.x == 0) a.tokens[b] = 0xffffffffu - (uint32_t)best;
-    (void)P;
-    return;
-  }
-#endif
   if (G == 1u) {
     row_single(a, (int)b, s);
     return;
   }
-  const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
-  const float rdraw = a.inline_draws ? a.inline_uniforms[b] : a.uniforms[b];
-  RowWs& ws = a.ws[b];
-  uint64_t* cand = a.cand + (uint64_t)b * kCandCap;
-  const Row row = make_row(a, (int)b);
-  const uint32_t per = ((a.vocab + G - 1u) / G + 15u) & ~15u;
-  if (P.flags & kGreedy) {
-    greedy_split(a, (int)b, sl, G, P, row, ws, s);
-  } else if ((P.flags & kTopK) && P.top_k <= 2048u) {
-    topk_split(a, (int)b, sl, G, P, row, ws, cand, rdraw, s);
-  } else if ((P.flags & kTopP) && !(P.flags & (kTopK | kPen)) && per <= 32u * kThreads * kChainMaxQ) {
-    topp_split(a, (int)b, sl, G, P, row, ws, cand, rdraw, s);
-  } else if (sl == 0) {
-    row_single(a, (int)b, s);
+  {
+    const RowParams& P = a.inline_rows ? a.inline_params[b] : a.params[b];
+    const uint32_t flags = P.flags;
+    const uint64_t top_k = P.top_k;
+    const uint32_t per = ((a.vocab + G - 1u) / G + 15u) & ~15u;
+    if (flags & kGreedy) {
+      greedy_split(a, (int)b, sl, G, s);
+    } else if ((flags & kTopK) && top_k <= 2048u) {
+      topk_split(a, (int)b, sl, G, s);
+    } else if ((flags & kTopP) && !(flags & (kTopK | kPen)) &&
+               per <= 32u * kThreads * kChainMaxQ) {
+      topp_split(a, (int)b, sl, G, s);
+    } else if (sl == 0) {
+      row_single(a, (int)b, s);
+    }
   }
-  // the last workgroup of the row to leave restores the coordination block
-  const uint32_t old = wg_arrive(&ws.exit_, s);
-  if (old == G - 1u && threadIdx.x == 0) {
-    ws.arrive = 0;
-    ws.bar = 0;
-    ws.cand_n = 0;
-    ws.status = 0;
-    for (uint32_t i = 0; i < G; ++i) ws.chain_flag[i] = 0;
-    __threadfence();
-    ws.exit_ = 0;
-    __threadfence();
-  }
+  row_exit(a, s);
 }
 }  // namespace lumen
