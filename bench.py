@@ -96,6 +96,50 @@ def cpu_baseline(w, uniforms, budget_s=20.0):
     return rows / el, rows, reps, el
 
 
+def cpu_baseline_threads(w, uniforms, threads, budget_s=10.0):
+    """The same rows on `threads` host threads (rows statically partitioned)."""
+    from oracle import oracle as o
+
+    lg = w.logits_f32()
+    ops = [o.Params(temperature=p.temperature, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p,
+                    repetition_penalty=p.repetition_penalty, presence_penalty=p.presence_penalty,
+                    frequency_penalty=p.frequency_penalty, repeat_last_n=p.repeat_last_n)
+           for p in w.params]
+    rows = 0
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        o.sample_batch(lg, ops, w.histories, uniforms, threads=threads)
+        rows += w.batch
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s / 2 or reps >= 5:
+            break
+    return rows / el, rows, reps, el
+
+
+def host_cores():
+    """CPU threads this process may use (the GPU box grants a share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit():
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def b1_latency(eng, draws=10_000):
     import torch
 
@@ -220,7 +264,15 @@ def main():
                                 "kind": "port",
                                 "sample": f"{w.name}: all {B} rows x {reps} passes "
                                           f"({rows} samples, {cel:.1f} s), same inputs, "
-                                          "single thread, oracle/sampling_ref.c -O2"}
+                                          "single thread, oracle/sampling_ref.c -O2",
+                                "cpu": cpu_model()}
+        nt = host_cores()
+        if nt > 1:
+            rate_mt, rows_mt, reps_mt, cel_mt = cpu_baseline_threads(w, u_host, nt)
+            line["cpu_baseline_all_cores"] = {
+                "value": round(rate_mt, 2), "unit": "samples/s", "cores": nt, "kind": "port",
+                "sample": f"{w.name}: all {B} rows x {reps_mt} passes ({rows_mt} samples, "
+                          f"{cel_mt:.1f} s), rows split over {nt} threads"}
     eng.close()
     print(json.dumps(line))
 

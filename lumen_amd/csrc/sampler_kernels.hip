@@ -1810,6 +1810,7 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
         }
         if (!ok) break;
         cc = y;
+        LUMEN_TICK(nb ? "slot_nb" : "slot", b);
       }
       s.misc_u[0] = j;
       s.red_f[0] = cc;
@@ -1825,6 +1826,7 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
     const uint32_t lo = si.lo + (id % kChainMaxQ) * chunk;
     float x[M];
     chain_load<M>(row, si, lo + t * (uint32_t)M, m1, x);
+    LUMEN_TICK(s.misc_size[j] == 0u ? (j == 0 ? "walk_norecord0" : "walk_norecord") : (j == 0 ? "walk_mismatch0" : "walk_mismatch"), b);
     c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
     LUMEN_TICK("walk_recomputed", b);
     j0 = j + 1u;
@@ -1974,6 +1976,7 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
     }
   }
   __syncthreads();
+  LUMEN_TICK("p_staged", b);
   float v_thr = tv;
   if (binned) {
     // first bin (from the top) where the running mass reaches the target
@@ -1998,6 +2001,7 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
       v_thr = fmaxf(tv, edge);
     }
   }
+  LUMEN_TICK("p_threshold", b);
   const float p_lo = tau ? __fdiv_rn(expf_glibc(__fsub_rn(v_thr, m1)), S1) : 0.f;
   if (t == 0) s.cnt = 0;
   __syncthreads();
