@@ -509,6 +509,10 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
                                                       float theta, EcssShared& sh, EstShared& es,
                                                       double* wsum, int nact = kThreads) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+#ifdef LUMEN_TICK_FINAL
+  __syncthreads();
+  LUMEN_TICK("e_x", 0);
+#endif
   double d = 0.0;
 #pragma unroll
   for (int j = 0; j < M; ++j) d += (double)x[j];
@@ -522,13 +526,24 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
   __syncthreads();
   const double p_start = (double)c + pre + inc - d;
   const double rel = (double)((t + 1) * M) * 0x1.0p-24 * 1.01 + 1e-9;
+#ifdef LUMEN_TICK_FINAL
+  LUMEN_TICK("e_scan", 0);
+#endif
   EstThread et;
   EcssResult r;
   if (!est_prepare<M>(x, p_start, d, rel, sh, es, et, nact)) {
     if (t == 0) es.fail = 2;  // structure did not fit (diagnostic only)
     return ecss_chunk<M>(c, x, mode, theta, sh);
   }
-  if (est_resolve<M>(c, x, mode, theta, et, sh, es, &r)) return r;
+#ifdef LUMEN_TICK_FINAL
+  LUMEN_TICK("e_prep", 0);
+#endif
+  if (est_resolve<M>(c, x, mode, theta, et, sh, es, &r)) {
+#ifdef LUMEN_TICK_FINAL
+    LUMEN_TICK("e_resolved", 0);
+#endif
+    return r;
+  }
   return ecss_chunk<M>(c, x, mode, theta, sh);
 }
 

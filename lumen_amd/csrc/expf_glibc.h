@@ -30,6 +30,15 @@ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
+// Per-workgroup LDS copy of the table: a divergent lookup in LDS costs an
+// LDS round trip instead of a vector memory load. Kernels that call
+// expf_glibc fill it with expf_table_init() followed by a barrier.
+__shared__ uint64_t g_exp2_lds[32];
+
+__device__ __forceinline__ void expf_table_init() {
+  if (threadIdx.x < 32) g_exp2_lds[threadIdx.x] = kExp2Tab[threadIdx.x];
+}
+
 __device__ __forceinline__ float expf_glibc(float x) {
   const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
   const double C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
@@ -49,7 +58,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
   uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd = __dsub_rn(kd, SHIFT);
   double r = __fma_rn(INVLN2N, xd, -kd);
-  uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+  uint64_t t = g_exp2_lds[ki & 31] + (ki << 47);
   double s = __longlong_as_double((long long)t);
   double z = __fma_rn(C0, r, C1);
   double r2 = __dmul_rn(r, r);

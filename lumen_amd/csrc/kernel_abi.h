@@ -57,6 +57,7 @@ enum RowStatus : uint32_t {
 
 constexpr int kInlineRows = 8;
 constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
+constexpr uint32_t kIdleBlock = 0xffffffffu;
 constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
 constexpr int kEstSharedBytes = 8192;  // upper bound of one parked run structure
@@ -103,8 +104,12 @@ struct KernelArgs {
   uint32_t* est;             // [B][kMaxSlices][kChainMaxQ] parked run structures
                              // (kEstSharedBytes each)
   uint64_t* cand;            // [B][kCandCap] candidate buffers
-  uint32_t slices;           // workgroups per row (G)
-  uint32_t xcd_rows;         // 1: place all slices of a row on one XCD
+  uint32_t slices;           // workgroups per row (G) when blk_map is NULL
+  uint32_t xcd_rows;         // 1: place all slices of a row on one XCD (blk_map NULL)
+  // Per-block placement: (row << 10) | (G << 5) | slice, or kIdleBlock. Rows
+  // get slice counts weighted by their path's cost, and a row's slices sit on
+  // one XCD. NULL: every row has `slices` workgroups, mapped as above.
+  const uint32_t* blk_map;
   uint32_t inline_rows;      // > 0: params come from inline_params
   uint32_t inline_draws;     // != 0: draws come from inline_uniforms
   float inline_uniforms[kInlineRows];

@@ -31,6 +31,80 @@ using lumen::RowParams;
 
 namespace {
 
+// Path a row takes in the kernel when it has G > 1 workgroups (mirrors the
+// dispatch in lumen_sample_rows).
+enum RowPath { kPathGreedy, kPathTopK, kPathTopP, kPathSingle };
+constexpr uint32_t kWgThreads = 1024;  // lumen_sample_rows workgroup size
+
+RowPath row_path(const RowParams& r, uint32_t V, uint32_t G) {
+  if (r.flags & lumen::kGreedy) return kPathGreedy;
+  if ((r.flags & lumen::kTopK) && r.top_k <= 2048u) return kPathTopK;
+  const uint32_t per = G ? ((V + G - 1u) / G + 15u) & ~15u : V;
+  if ((r.flags & lumen::kTopP) && !(r.flags & (lumen::kTopK | lumen::kPen)) &&
+      per <= 32u * kWgThreads * (uint32_t)lumen::kChainMaxQ)
+    return kPathTopP;
+  return kPathSingle;
+}
+
+// Workgroups per row, weighted by the cost of the row's path (a top-p row
+// reads its row twice and has the longest finisher; a greedy row reads it
+// once and finishes in a few microseconds), and their placement: with
+// blocks dispatched to the 8 XCDs round-robin, block ids x, x + 8, ... land
+// on XCD x, so each row's slices are packed into one XCD's list. The total
+// never exceeds the resident capacity, so every row's workgroups are
+// co-resident. Returns the grid size; map[block] = (row << 10) | (G << 5) |
+// slice, or kIdleBlock.
+uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t cap,
+                     std::vector<uint32_t>& map) {
+  const uint32_t B = (uint32_t)rows.size();
+  const uint32_t kX = 8;
+  const uint32_t bin_cap = cap / kX;
+  std::vector<uint32_t> G(B, 1), w(B, 0);
+  const uint32_t gmin_topp =
+      (V + 32u * kWgThreads * (uint32_t)lumen::kChainMaxQ - 1u) /
+      (32u * kWgThreads * (uint32_t)lumen::kChainMaxQ);
+  uint64_t wsum = 0;
+  uint32_t fixed = 0;
+  for (uint32_t b = 0; b < B; ++b) {
+    switch (row_path(rows[b], V, lumen::kMaxSlices)) {
+      case kPathGreedy: w[b] = 2; break;
+      case kPathTopK: w[b] = 3; break;
+      case kPathTopP: w[b] = 6; break;
+      default: w[b] = 0; ++fixed; break;  // exact single-workgroup row
+    }
+    wsum += w[b];
+  }
+  const uint32_t spare = cap > fixed ? cap - fixed : 0;
+  for (uint32_t b = 0; b < B; ++b) {
+    if (!w[b]) continue;
+    uint64_t g = wsum ? ((uint64_t)spare * w[b] + wsum / 2) / wsum : 1;
+    G[b] = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(g, lumen::kMaxSlices));
+    if (row_path(rows[b], V, G[b]) == kPathTopP && G[b] < gmin_topp) G[b] = 1;
+  }
+  // pack rows (largest first) into the XCD lists
+  std::vector<uint32_t> order(B);
+  for (uint32_t b = 0; b < B; ++b) order[b] = b;
+  std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) { return G[x] > G[y]; });
+  std::vector<std::vector<uint32_t>> bins(kX);
+  for (uint32_t b : order) {
+    uint32_t best = 0;
+    for (uint32_t x = 1; x < kX; ++x)
+      if (bins[x].size() < bins[best].size()) best = x;
+    uint32_t free_slots = bin_cap > bins[best].size() ? bin_cap - (uint32_t)bins[best].size() : 0;
+    uint32_t g = std::min(G[b], std::max<uint32_t>(free_slots, 1u));
+    if (g > 1 && row_path(rows[b], V, g) == kPathSingle) g = 1;
+    if (g > 1 && row_path(rows[b], V, g) == kPathTopP && g < gmin_topp) g = 1;
+    for (uint32_t sl = 0; sl < g; ++sl) bins[best].push_back((b << 10) | (g << 5) | sl);
+  }
+  size_t depth = 0;
+  for (const auto& v : bins) depth = std::max(depth, v.size());
+  const uint32_t nblocks = (uint32_t)depth * kX;
+  map.assign(nblocks, lumen::kIdleBlock);
+  for (uint32_t x = 0; x < kX; ++x)
+    for (size_t k = 0; k < bins[x].size(); ++k) map[x + kX * k] = bins[x][k];
+  return nblocks;
+}
+
 constexpr float kF32Eps = 1.1920929e-7f;  // f32::EPSILON
 
 struct DevBuf {
@@ -58,6 +132,7 @@ struct lumen_sampler {
   bool staged_pending = false;
   std::vector<uint32_t> ids, cnts, offs;
   std::vector<uint32_t> tmp;
+  std::vector<uint32_t> blk_map;  // per-block placement of the current call
   std::vector<char> img, last_img;  // static staging block: current / on the device
 };
 
@@ -347,6 +422,22 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
   ka.trace = reinterpret_cast<lumen::RowTrace*>(bt->trace);
   ka.pen_out = bt->penalized_out;
 
+  // Workgroups per row: enough to occupy every CU once (all co-resident),
+  // at most kMaxSlices. With 8+ rows, a row's slices share one XCD.
+  uint32_t G = 1;
+  const uint32_t padded = B >= 8 ? ((B + 7u) / 8u) * 8u : B;
+  if (s->max_resident > 0 && std::getenv("LUMEN_SAMPLER_SINGLE") == nullptr)
+    G = std::max<uint32_t>(1u, std::min<uint32_t>(lumen::kMaxSlices,
+                                                  (uint32_t)s->max_resident / padded));
+  ka.slices = G;
+  ka.xcd_rows = (B >= 8 && G > 1) ? 1u : 0u;
+  uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
+  if (G > 1 && B >= 8 && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
+    nblocks = plan_blocks(rows, V, (uint32_t)s->max_resident, s->blk_map);
+    ka.slices = lumen::kMaxSlices;  // buffers are sized for the largest G
+  } else {
+    s->blk_map.clear();
+  }
   // Staging. Two blocks share one pinned host buffer and one device buffer:
   //   static block [params][offs][ids][cnts]: copied only when its bytes
   //                differ from what the device buffer already holds;
@@ -358,7 +449,8 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
   const size_t off_offs = inl ? 0 : a16(sizeof(RowParams) * B);
   const size_t off_ids = off_offs + (host_csr ? sizeof(uint32_t) * (B + 1) : 0);
   const size_t off_cnts = off_ids + (host_csr ? sizeof(uint32_t) * s->ids.size() : 0);
-  const size_t static_sz = a16(off_cnts + (host_csr ? sizeof(uint32_t) * s->cnts.size() : 0));
+  const size_t off_map = a16(off_cnts + (host_csr ? sizeof(uint32_t) * s->cnts.size() : 0));
+  const size_t static_sz = a16(off_map + sizeof(uint32_t) * s->blk_map.size());
   const bool draw_block = !bt->uniforms_dev && !inl;
   const size_t total = static_sz + (draw_block ? sizeof(float) * B : 0);
   if (inl) {
@@ -374,6 +466,8 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
   if (total > 0) {
     s->img.assign(static_sz, 0);
     if (!inl) std::memcpy(s->img.data(), rows.data(), sizeof(RowParams) * B);
+    if (!s->blk_map.empty())
+      std::memcpy(s->img.data() + off_map, s->blk_map.data(), sizeof(uint32_t) * s->blk_map.size());
     if (host_csr) {
       std::memcpy(s->img.data() + off_offs, s->offs.data(), sizeof(uint32_t) * (B + 1));
       if (!s->ids.empty()) {
@@ -413,6 +507,7 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
     }
     char* dp = static_cast<char*>(s->stage.p);
     if (!inl) ka.params = reinterpret_cast<const RowParams*>(dp);
+    if (!s->blk_map.empty()) ka.blk_map = reinterpret_cast<const uint32_t*>(dp + off_map);
     if (draw_block) ka.uniforms = reinterpret_cast<const float*>(dp + static_sz);
     if (host_csr) {
       ka.hist_off = reinterpret_cast<const uint32_t*>(dp + off_offs);
@@ -432,16 +527,6 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
     ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
     ka.pen_stride = stride;
   }
-  // Workgroups per row: enough to occupy every CU once (all co-resident),
-  // at most kMaxSlices. With 8+ rows, a row's slices share one XCD.
-  uint32_t G = 1;
-  const uint32_t padded = B >= 8 ? ((B + 7u) / 8u) * 8u : B;
-  if (s->max_resident > 0 && std::getenv("LUMEN_SAMPLER_SINGLE") == nullptr)
-    G = std::max<uint32_t>(1u, std::min<uint32_t>(lumen::kMaxSlices,
-                                                  (uint32_t)s->max_resident / padded));
-  ka.slices = G;
-  ka.xcd_rows = (B >= 8 && G > 1) ? 1u : 0u;
-  const uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
   if (G > 1) {
     const size_t ws_bytes = sizeof(lumen::RowWs) * B;
     if (s->ws.cap < ws_bytes) {

@@ -31,7 +31,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "ecss.h"
 #include "expf_glibc.h"
 #include "kernel_abi.h"
 
@@ -40,12 +39,12 @@
 // once when that row's result is written.
 #ifdef LUMEN_TIMING
 #include <cstdio>
-__shared__ unsigned long long g_ticks[40];
-__shared__ const char* g_tick_names[40];
+__shared__ unsigned long long g_ticks[26];
+__shared__ const char* g_tick_names[26];
 __shared__ int g_nticks;
 #define LUMEN_TICK(label, b)                                         \
   do {                                                              \
-    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 40) {            \
+    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 26) {            \
       g_ticks[g_nticks] = wall_clock64();                           \
       g_tick_names[g_nticks++] = label;                             \
     }                                                               \
@@ -53,6 +52,10 @@ __shared__ int g_nticks;
 #define LUMEN_TICK_INIT() \
   do {                    \
     if (threadIdx.x == 0) g_nticks = 0; \
+  } while (0)
+#define LUMEN_TICK_RESET(b) \
+  do {                      \
+    if (threadIdx.x == 0 && (b) == 0) g_nticks = 0; \
   } while (0)
 #define LUMEN_TICK_DUMP(b)                                                       \
   do {                                                                          \
@@ -64,8 +67,11 @@ __shared__ int g_nticks;
 #else
 #define LUMEN_TICK(label, b) do { } while (0)
 #define LUMEN_TICK_INIT() do { } while (0)
+#define LUMEN_TICK_RESET(b) do { } while (0)
 #define LUMEN_TICK_DUMP(b) do { } while (0)
 #endif
+
+#include "ecss.h"
 
 namespace lumen {
 
@@ -780,6 +786,10 @@ __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a,
                                   Smem& s, RowTrace& tr) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
+#ifdef LUMEN_TICK_FINAL
+  LUMEN_TICK_RESET(0);
+  LUMEN_TICK("final_start", 0);
+#endif
   // min-p (sampling.rs:976-994)
   bool mmask = false;
   float bound = 0.f;
@@ -1719,8 +1729,13 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
     // The incoming sum is only estimated here (other slices' exp-sums); the
     // rounding drift of a long f32 sum is typically ~1e-5 relative. A wrong
     // guess only costs the exact recomputation in chain_walk.
+    // The exact f32 running sum drifts below its f64 estimate: addends are
+    // rounded onto the accumulator's grid, and the small ones are lost. The
+    // drift reaches ~5e-4 relative after 250K summands in logit rows, so the
+    // boundary margin grows with the position in the row.
+    const double rel = 4e-5 + 3e-9 * (double)(sc.lo + q * chunk);
     EstThread et;
-    if (est_prepare<M>(x, pt, d, 4e-5, s.ecss, s.est, et,
+    if (est_prepare<M>(x, pt, d, rel, s.ecss, s.est, et,
                        (int)min((uint32_t)kThreads, ((sc.hi - (sc.lo + q * chunk)) + (uint32_t)M - 1u) / (uint32_t)M))) {
       fits |= 1u << q;
       park_record<M>(est_slot(a, b, sl, q), s.est);
@@ -1810,7 +1825,6 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
         }
         if (!ok) break;
         cc = y;
-        LUMEN_TICK(nb ? "slot_nb" : "slot", b);
       }
       s.misc_u[0] = j;
       s.red_f[0] = cc;
@@ -1948,10 +1962,14 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
   // the row to the exact path.
   constexpr uint32_t kBins = 512;
   float* hmass = reinterpret_cast<float*>(s.H);
+  // one histogram per wave (in the list area B, free until the window is
+  // built), so that atomics only collide inside a wave
+  float* hwave = reinterpret_cast<float*>(s.Bk) + (t >> 6) * kBins;
   const float span = tau ? __fsub_rn(m1, tv) : 0.f;
   const bool binned = tau && span > 0.f;
   const float inv_w = binned ? __fdiv_rn((float)kBins, span) : 0.f;
-  for (uint32_t i = t; i < kBins; i += kThreads) hmass[i] = 0.f;
+  for (uint32_t i = t; i < kBins * (uint32_t)kWaves; i += kThreads)
+    reinterpret_cast<float*>(s.Bk)[i] = 0.f;
   __syncthreads();
   // stage the candidates in LDS as (exp(v - m1) bits << 32) | index, all
   // loads in flight together; bin the exp-mass of those >= tau
@@ -1963,6 +1981,15 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
       const uint32_t j = base + (uint32_t)q * kThreads + t;
       c[q] = j < nc ? cand[j] : 0ull;
     }
+#ifdef LUMEN_TIMING
+    {
+      uint64_t acc = 0;
+      for (int q = 0; q < 8; ++q) acc ^= c[q];
+      if (acc == 0x123456789ull) s.misc_u[0] = 1;
+      __syncthreads();
+      LUMEN_TICK("p_cand_loaded", b);
+    }
+#endif
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const uint32_t j = base + (uint32_t)q * kThreads + t;
@@ -1971,9 +1998,17 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
         const float x = expf_glibc(__fsub_rn(v, m1));
         s.A[j] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)c[q];
         if (binned && v >= tv)
-          atomicAdd(&hmass[min(kBins - 1u, (uint32_t)(__fsub_rn(m1, v) * inv_w))], x);
+          atomicAdd(&hwave[min(kBins - 1u, (uint32_t)(__fsub_rn(m1, v) * inv_w))], x);
       }
     }
+  }
+  __syncthreads();
+  LUMEN_TICK("p_cand_binned", b);
+  for (uint32_t i = t; i < kBins; i += kThreads) {
+    float m = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kWaves; ++wv) m += reinterpret_cast<const float*>(s.Bk)[wv * kBins + i];
+    hmass[i] = m;
   }
   __syncthreads();
   LUMEN_TICK("p_staged", b);
@@ -2047,8 +2082,22 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
 // Row and slice of this workgroup. With xcd_rows, blocks are dispatched to
 // the 8 XCDs round-robin: a row's slices stay on one XCD so its
 // coordination traffic stays in that XCD's L2.
-__device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint32_t& sl) {
-  const uint32_t G = a.slices;
+__device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint32_t& sl,
+                                          uint32_t& G) {
+  if (a.blk_map) {
+    const uint32_t m = a.blk_map[blockIdx.x];
+    if (m == kIdleBlock) {
+      b = 0xffffffffu;
+      sl = 0;
+      G = 1;
+      return;
+    }
+    b = m >> 10;
+    G = (m >> 5) & 31u;
+    sl = m & 31u;
+    return;
+  }
+  G = a.slices;
   if (a.xcd_rows) {
     const uint32_t xcd = blockIdx.x & 7u, j = blockIdx.x >> 3;
     b = xcd + 8u * (j / G);
@@ -2063,9 +2112,8 @@ __device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint
 // row is derived again from the block index, so nothing has to stay live
 // across the path calls.
 __device__ __attribute__((noinline)) void row_exit(const KernelArgs& a, Smem& s) {
-  uint32_t b, sl;
-  block_row(a, b, sl);
-  const uint32_t G = a.slices;
+  uint32_t b, sl, G;
+  block_row(a, b, sl, G);
   RowWs& ws = a.ws[b];
   const uint32_t old = wg_arrive(&ws.exit_, s);
   if (old == G - 1u && threadIdx.x == 0) {
@@ -2090,9 +2138,10 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
       *reinterpret_cast<const KernelArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
   __shared__ Smem s;
   LUMEN_TICK_INIT();
-  const uint32_t G = a.slices;
-  uint32_t b, sl;
-  block_row(a, b, sl);
+  expf_table_init();
+  __syncthreads();
+  uint32_t b, sl, G;
+  block_row(a, b, sl, G);
   if (b >= a.batch) return;
   if (G == 1u) {
     row_single(a, (int)b, s);
