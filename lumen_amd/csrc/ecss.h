@@ -356,9 +356,16 @@ __device__ __forceinline__ bool est_prepare(const float (&x)[M], double p_start,
     nb += sh.red_b[i];
   }
   et.run = before_w + __popcll(bm & ((1ull << lane) - 1ull));
+#ifdef LUMEN_TICK_FINAL
+  LUMEN_TICK("p1cn", 0);
+#endif
   SegVal v{et.boundary, et.own};
   SegVal prev;
   SegVal inc = seg_scan_incl(v, sh, es, &prev);
+#ifdef LUMEN_TICK_FINAL
+  LUMEN_TICK("p2sc", 0);
+#endif
+
   et.excl = (t == 0) ? PMap{0u, 0u} : prev.m;
   const bool fits = nb <= kEstMaxB && nb * M <= kEstBx;
   if (fits) {
@@ -395,56 +402,142 @@ __device__ __forceinline__ bool est_resolve(float c_in, const float (&x)[M], int
                                             const EstThread& et, EcssShared& sh, EstShared& es,
                                             EcssResult* res) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  if (t == 0) {
+  if (w == 0) {
+    const int nb = es.nb;
+    // Up to 63 boundaries: lane k holds run k and boundary k in registers
+    // (one LDS round trip), and the walk reads them with v_readlane, so the
+    // sequential part has no memory latency. All lanes run the walk (the
+    // values are uniform); lane 0 publishes it.
+    const bool regs = nb < 64;
+    uint32_t sb_r = 0, a0_r = 0, a1_r = 0, bp_r = 0;
+    float bx_r[M];
+#pragma unroll
+    for (int q = 0; q < M; ++q) bx_r[q] = 0.f;
+    if (regs) {
+      if (lane <= nb) {
+        sb_r = es.seg_bin[lane];
+        a0_r = es.seg_tot[lane].a0;
+        a1_r = es.seg_tot[lane].a1;
+      }
+      if (lane < nb) {
+        bp_r = es.bpos[lane];
+#pragma unroll
+        for (int q = 0; q < M; ++q) bx_r[q] = es.bx[lane * M + q];
+      }
+    }
     float c = c_in;
     int fail = 0, hit_seg = -1, hit_pos = -1;
     float before = 0.f, cseg = 0.f;
-    const int nb = es.nb;
-    for (int k = 0; k <= nb && !fail && hit_seg < 0 && hit_pos < 0; ++k) {
-      const uint32_t sb = es.seg_bin[k];
-      if (sb != kEmptyRun) {
+#ifdef LUMEN_TICK_FINAL
+    {
+      float acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < M; ++q) acc += bx_r[q];
+      if (acc == 1234.5f && sb_r == 7u && a0_r == 3u && a1_r == 5u && bp_r == 9u) es.fail = 7;
+      LUMEN_TICK("r0pf", 0);
+    }
+#endif
+    if (regs) {
+      // Branch-free walk. The only dependent chain per boundary is the
+      // parity-selected run increment and the M sequential adds; the checks
+      // and the first stop (failure, hit inside a run, hit inside a
+      // boundary) are recorded with selects off that chain.
+      bool stopped = false;
+      for (int k = 0; k <= nb; ++k) {
+        const uint32_t sb = (uint32_t)__builtin_amdgcn_readlane((int)sb_r, k);
+        const uint32_t m0 = (uint32_t)__builtin_amdgcn_readlane((int)a0_r, k);
+        const uint32_t m1 = (uint32_t)__builtin_amdgcn_readlane((int)a1_r, k);
         const uint32_t cb = __float_as_uint(c);
-        if ((cb & 0xff800000u) != sb) {
-          fail = 1;
-          break;
-        }
-        const PMap m = es.seg_tot[k];
-        const uint32_t inc = (cb & 1u) ? m.a1 : m.a0;
+        const uint32_t inc = (cb & 1u) ? m1 : m0;
         const uint32_t nbits = cb + inc;
-        if (inc >= kSat || nbits >= sb + 0x00800000u) {
-          fail = 1;
-          break;
-        }
-        if (mode != kEcssSum && ecss_cond(mode, __uint_as_float(nbits), theta)) {
+        const bool run = sb != kEmptyRun;
+        const bool bad = run && ((cb & 0xff800000u) != sb || inc >= kSat || nbits >= sb + 0x00800000u);
+        const bool hs = run && !bad && mode != kEcssSum && ecss_cond(mode, __uint_as_float(nbits), theta);
+        if (!stopped && bad) fail = 1;
+        if (!stopped && hs) {
           hit_seg = k;
           cseg = c;
-          break;
         }
-        c = __uint_as_float(nbits);
-      }
-      if (k == nb) break;
-      float y = c, p = c;
-      int j = M;
+        stopped = stopped || bad || hs;
+        const float cr = run ? __uint_as_float(nbits) : c;
+        float ys[M];
+        float y = cr;
 #pragma unroll
-      for (int q = 0; q < M; ++q) {
-        if (j == M) {
-          p = y;
-          y = __fadd_rn(y, es.bx[k * M + q]);
-          if (mode != kEcssSum && ecss_cond(mode, y, theta)) j = q;
+        for (int q = 0; q < M; ++q) {
+          y = __fadd_rn(y, __int_as_float(__builtin_amdgcn_readlane(
+                              __float_as_int(bx_r[q]), k < nb ? k : 0)));
+          ys[q] = y;
         }
+        if (mode != kEcssSum && k < nb) {
+          int j = M;
+#pragma unroll
+          for (int q = M - 1; q >= 0; --q) j = ecss_cond(mode, ys[q], theta) ? q : j;
+          if (!stopped && j < M) {
+            hit_pos = (int)__builtin_amdgcn_readlane((int)bp_r, k) * M + j;
+            float pb = cr;
+#pragma unroll
+            for (int q = 1; q < M; ++q) pb = (q == j) ? ys[q - 1] : pb;
+            before = pb;
+            float yh = ys[0];
+#pragma unroll
+            for (int q = 1; q < M; ++q) yh = (q == j) ? ys[q] : yh;
+            c = yh;
+            stopped = true;
+          }
+        }
+        if (!stopped) c = k < nb ? y : cr;
       }
-      c = y;
-      if (j < M) {
-        hit_pos = (int)es.bpos[k] * M + j;
-        before = p;
+    } else {
+      for (int k = 0; k <= nb && !fail && hit_seg < 0 && hit_pos < 0; ++k) {
+        const uint32_t sb = es.seg_bin[k];
+        if (sb != kEmptyRun) {
+          const uint32_t cb = __float_as_uint(c);
+          if ((cb & 0xff800000u) != sb) {
+            fail = 1;
+            break;
+          }
+          const uint32_t inc = (cb & 1u) ? es.seg_tot[k].a1 : es.seg_tot[k].a0;
+          const uint32_t nbits = cb + inc;
+          if (inc >= kSat || nbits >= sb + 0x00800000u) {
+            fail = 1;
+            break;
+          }
+          if (mode != kEcssSum && ecss_cond(mode, __uint_as_float(nbits), theta)) {
+            hit_seg = k;
+            cseg = c;
+            break;
+          }
+          c = __uint_as_float(nbits);
+        }
+        if (k == nb) break;
+        float y = c, p = c;
+        int j = M;
+#pragma unroll
+        for (int q = 0; q < M; ++q) {
+          if (j == M) {
+            p = y;
+            y = __fadd_rn(y, es.bx[k * M + q]);
+            if (mode != kEcssSum && ecss_cond(mode, y, theta)) j = q;
+          }
+        }
+        c = y;
+        if (j < M) {
+          hit_pos = (int)es.bpos[k] * M + j;
+          before = p;
+        }
       }
     }
-    es.fail = fail;
-    es.hit_seg = hit_seg;
-    es.hit_pos = hit_pos;
-    es.c_out = c;
-    es.c_seg = cseg;
-    es.before = before;
+    if (lane == 0) {
+#ifdef LUMEN_TICK_FINAL
+      LUMEN_TICK("r1wk", 0);
+#endif
+      es.fail = fail;
+      es.hit_seg = hit_seg;
+      es.hit_pos = hit_pos;
+      es.c_out = c;
+      es.c_seg = cseg;
+      es.before = before;
+    }
   }
   __syncthreads();
   const int fail = es.fail, hit_seg = es.hit_seg, hit_pos = es.hit_pos;

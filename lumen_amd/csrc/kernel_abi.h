@@ -58,7 +58,8 @@ enum RowStatus : uint32_t {
 constexpr int kInlineRows = 8;
 constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
 constexpr uint32_t kIdleBlock = 0xffffffffu;
-constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
+constexpr int kCandCap = 8192;
+constexpr int kMassBins = 512;       // top-p window planning bins      // per-row candidate buffer (entries)
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
 constexpr int kEstSharedBytes = 8192;  // upper bound of one parked run structure
 
@@ -72,8 +73,7 @@ struct RowWs {
   uint32_t cand_n;       // candidates appended
   uint32_t status;       // row failure bits
   uint32_t pad[3];
-  uint32_t chain_flag[kMaxSlices];
-  float chain_c[kMaxSlices];
+  uint32_t part_words[kMaxSlices * kChainMaxQ];  // parked record sizes (32-bit words)
   float part_max[kMaxSlices];
   uint32_t part_nan[kMaxSlices];
   uint64_t part_arg[kMaxSlices];
@@ -104,6 +104,7 @@ struct KernelArgs {
   uint32_t* est;             // [B][kMaxSlices][kChainMaxQ] parked run structures
                              // (kEstSharedBytes each)
   uint64_t* cand;            // [B][kCandCap] candidate buffers
+  float* hist;               // [B][kMaxSlices][kMassBins] candidate exp-mass per logit bin
   uint32_t slices;           // workgroups per row (G) when blk_map is NULL
   uint32_t xcd_rows;         // 1: place all slices of a row on one XCD (blk_map NULL)
   // Per-block placement: (row << 10) | (G << 5) | slice, or kIdleBlock. Rows

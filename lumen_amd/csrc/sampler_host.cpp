@@ -126,6 +126,7 @@ struct lumen_sampler {
   DevBuf ws;    // [B] RowWs, zeroed at allocation, self-resetting afterwards
   DevBuf cand;  // [B][kCandCap] candidate buffers
   DevBuf est;   // [B][kMaxSlices][kChainMaxQ] parked run structures
+  DevBuf hist;  // [B][kMaxSlices][kMassBins] candidate mass histograms
   int cu_count = 0;
   int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
   hipEvent_t staged = nullptr;  // recorded after the last staging copy
@@ -331,6 +332,7 @@ void lumen_sampler_destroy(lumen_sampler* s) {
   if (s->ws.p) (void)hipFree(s->ws.p);
   if (s->cand.p) (void)hipFree(s->cand.p);
   if (s->est.p) (void)hipFree(s->est.p);
+  if (s->hist.p) (void)hipFree(s->hist.p);
   if (s->staged) (void)hipEventDestroy(s->staged);
   if (s->module) (void)hipModuleUnload(s->module);
   delete s;
@@ -543,6 +545,9 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
     ka.ws = static_cast<lumen::RowWs*>(s->ws.p);
     ka.cand = static_cast<uint64_t*>(s->cand.p);
     ka.est = static_cast<uint32_t*>(s->est.p);
+    rc = ensure_dev(s->hist, sizeof(float) * lumen::kMaxSlices * lumen::kMassBins * B);
+    if (rc != LUMEN_OK) return rc;
+    ka.hist = static_cast<float*>(s->hist.p);
     // Every wait inside the kernel is bounded and reports a row failure on
     // timeout, so an ordinary launch is safe; a cooperative launch (which
     // guarantees co-residency of the grid) costs ~18 us more per call and is

@@ -515,8 +515,10 @@ constexpr uint32_t kBucketMax = 256;  // largest bucket ranked by direct countin
 // order the atomic scatter left inside the bucket. When a bucket holds
 // more than kBucketMax keys the radix sort takes over.
 __device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n,
-                                                          Smem& s) {
+                                                          uint64_t diff_hint, Smem& s) {
   const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  uint64_t diff = diff_hint;  // a superset of the bits in which keys differ, or 0
+  if (!diff) {
   uint64_t o = 0ull, an = ~0ull;
   for (uint32_t j = t; j < n; j += kThreads) {
     o |= a[j];
@@ -537,8 +539,9 @@ __device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t*
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) ra &= red[i];
   __syncthreads();
-  const uint64_t diff = ro ^ ra;  // bits that differ between some keys
-  if (!diff) return;              // all keys equal
+  diff = ro ^ ra;     // bits that differ between some keys
+  if (!diff) return;  // all keys equal
+  }
   const uint32_t hb = 63u - (uint32_t)__clzll((long long)diff);
   const uint32_t sh = hb >= 11u ? hb - 11u : 0u;
   uint32_t* H = s.H;
@@ -601,12 +604,18 @@ __device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t*
 
 // Ascending sort of a[0..n) in LDS. With a free second buffer `tmp` (n
 // entries) lists above 256 entries take the bucket sort.
-__device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n, uint64_t* tmp, Smem& s) {
+__device__ __forceinline__ void sort_u64_asc(uint64_t* a, uint32_t n, uint64_t* tmp, Smem& s,
+                                             uint64_t diff_hint = 0) {
   if (n > 256u && tmp) {
-    bucket_sort_u64(a, tmp, n, s);
+    bucket_sort_u64(a, tmp, n, diff_hint, s);
     return;
   }
   sort_u64_bitonic(a, n);
+}
+
+// All-ones mask covering every value below n (n >= 1).
+__device__ __forceinline__ uint32_t span_mask(uint32_t n) {
+  return n <= 1u ? 0u : 0xffffffffu >> __clz(n - 1u);
 }
 
 // Wave-aggregated append into an LDS list; returns nothing, counts all.
@@ -782,8 +791,10 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
 
 // Final stage over the LDS list A (entries (idx << 32) | key, ascending idx,
 // n entries, every entry alive). Applies min-p, temperature, softmax, draw.
+// known_max: the largest logit of the list when the caller knows it (the
+// list is NaN-free then), NaN otherwise.
 __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a, const RowParams P, uint32_t n, float r,
-                                  Smem& s, RowTrace& tr) {
+                                  Smem& s, RowTrace& tr, float known_max) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
 #ifdef LUMEN_TICK_FINAL
@@ -793,10 +804,14 @@ __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a,
   // min-p (sampling.rs:976-994)
   bool mmask = false;
   float bound = 0.f;
+  const bool known = !is_nan(known_max);
   if (P.flags & kMinP) {
-    float m = kNegInf;
-    for (uint32_t j = threadIdx.x; j < n; j += kThreads) m = rmax(m, lv(j));
-    m = block_rmax(m, s);
+    float m = known_max;
+    if (!known) {
+      m = kNegInf;
+      for (uint32_t j = threadIdx.x; j < n; j += kThreads) m = rmax(m, lv(j));
+      m = block_rmax(m, s);
+    }
     if (is_finite(m)) {
       mmask = true;
       bound = __fadd_rn(m, P.log_min_p);
@@ -809,17 +824,21 @@ __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a,
   };
   float m3 = kNegInf;
   uint32_t nan3 = 0;
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
-    float w = wv(j);
-    m3 = rmax(m3, w);
-    nan3 |= is_nan(w) ? 1u : 0u;
+  if (known && !(mmask && known_max < bound)) {
+    // x -> x * inv_temp (inv_temp > 0) is monotone under rounding
+    m3 = __fmul_rn(known_max, P.inv_temp);
+  } else {
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
+      float w = wv(j);
+      m3 = rmax(m3, w);
+      nan3 |= is_nan(w) ? 1u : 0u;
+    }
+    // tokens outside the list are -inf * inv_temp: they only matter when the
+    // list has no finite value at all (uniform branch over all V tokens)
+    m3 = block_rmax(m3, s);
+    nan3 = block_or_u32(nan3, s);
   }
-  // tokens outside the list are -inf * inv_temp: they only matter when the
-  // list has no finite value at all (uniform branch over all V tokens)
-  LUMEN_TICK("fin_m3_local", 0);
-  m3 = block_rmax(m3, s);
-  nan3 = block_or_u32(nan3, s);
-  LUMEN_TICK("fin_m3_block", 0);
+  LUMEN_TICK("fin_m3", 0);
   tr.final_max = m3;
   if (!is_finite(m3)) {
     tr.path |= 16u;
@@ -858,7 +877,8 @@ __device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a,
 // (idx << 32) | key, ascending idx (sampling.rs:502-526): top-p on the list
 // (unless already applied), min-p, temperature, softmax, draw.
 __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
-                           bool topp_done, float rdraw, Smem& s, RowTrace& tr) {
+                           bool topp_done, float rdraw, Smem& s, RowTrace& tr,
+                           float known_max = __builtin_nanf("")) {
   const int t = threadIdx.x;
   const uint32_t V = a.vocab;
   tr.path |= 2u;
@@ -951,7 +971,7 @@ __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const Row
     nlist = nk;
   }
   LUMEN_TICK("small_before_final", b);
-  uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr);
+  uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr, known_max);
   LUMEN_TICK("small_after_final", b);
   write_result(a, b, tok, tr);
 }
@@ -1739,6 +1759,8 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
                        (int)min((uint32_t)kThreads, ((sc.hi - (sc.lo + q * chunk)) + (uint32_t)M - 1u) / (uint32_t)M))) {
       fits |= 1u << q;
       park_record<M>(est_slot(a, b, sl, q), s.est);
+      if (threadIdx.x == 0)
+        a.ws[b].part_words[sl * kChainMaxQ + q] = record_words<M>((uint32_t)s.est.nb);
     }
     __syncthreads();
   }
@@ -1746,20 +1768,19 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
 }
 
 // Exact softmax sum of the row from the parked records (last workgroup of
-// the row). The records of all slots (slice i, sub-chunk q, in row order)
-// are gathered into the list area with one bulk copy; thread 0 then walks
-// runs and boundary summands in order. A slot without a record, or whose
-// record does not match the exact running sum (wrong binade guess), is
-// recomputed by the whole workgroup with the iterative method, and the walk
-// resumes after it.
+// the row). Slots are (slice i, sub-chunk q) in row order; their record
+// sizes come from the coordination block. chain_gather_issue() copies every
+// record into `words` (up to `cap` words) with one bulk copy; chain_walk()
+// then walks runs and boundary summands in order on one wave. A slot without
+// a record, or whose record does not match the exact running sum (a wrong
+// binade guess: the slice prefix was only estimated), is recomputed by the
+// whole workgroup with the iterative method, and the walk resumes after it.
 template <int M>
-__device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t G, const Row& row,
-                                           float m1, RowWs& ws, Smem& s) {
+__device__ __forceinline__ void chain_slots(const KernelArgs& a, int b, uint32_t G, RowWs& ws,
+                                            uint32_t cap, Smem& s) {
   const uint32_t t = threadIdx.x, V = a.vocab;
   const uint32_t chunk = (uint32_t)kThreads * M;
   uint32_t* off = s.misc_slot;  // [0..kSlots]: record offsets; kSlots + j: slot id
-  uint32_t* words = reinterpret_cast<uint32_t*>(s.A);
-  // slot list, record sizes and offsets (one wave)
   if (t < 64u) {
     uint32_t id = 0xffffffffu, size = 0;
     uint32_t n = 0;
@@ -1770,20 +1791,29 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
       for (uint32_t q = 0; q < nq; ++q, ++n) {
         if (n == t) {
           id = i * kChainMaxQ + q;
-          if ((fi >> q) & 1u) size = record_words<M>(est_slot(a, b, i, q)[0]);
+          if ((fi >> q) & 1u) size = ws.part_words[id];
         }
       }
     }
     const uint32_t inc = wave_scan_incl(size, 0u, op_add_u32);
+    // records beyond the area count as missing (recomputed)
+    if (inc > cap) size = 0;
+    const uint32_t inc2 = wave_scan_incl(size, 0u, op_add_u32);
     if (t < (uint32_t)kSlots) {
-      off[t] = inc - size;
+      off[t] = inc2 - size;
       off[kSlots + t] = id;
       s.misc_size[t] = size;
     }
     if (t == 0) s.misc_u[3] = n;
-    if (t == 63u) s.misc_u[2] = inc;
+    if (t == 63u) s.misc_u[2] = inc2;
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void chain_gather_issue(const KernelArgs& a, int b, uint32_t* words,
+                                                   Smem& s) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t* off = s.misc_slot;
   const uint32_t nslots = s.misc_u[3];
   const uint32_t total = s.misc_u[2];
   for (uint32_t w = t; w < total; w += kThreads) {
@@ -1792,8 +1822,15 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
     const uint32_t id = off[kSlots + j];
     words[w] = est_slot(a, b, id / kChainMaxQ, id % kChainMaxQ)[w - off[j]];
   }
-  __syncthreads();
-  LUMEN_TICK("p_prefetched", b);
+}
+
+template <int M>
+__device__ __forceinline__ float chain_walk(const KernelArgs& a, int b, uint32_t G, const Row& row,
+                                            float m1, const uint32_t* words, Smem& s) {
+  const uint32_t t = threadIdx.x, V = a.vocab;
+  const uint32_t chunk = (uint32_t)kThreads * M;
+  const uint32_t* off = s.misc_slot;
+  const uint32_t nslots = s.misc_u[3];
   float c = 0.f;
   uint32_t j0 = 0;
   while (j0 < nslots) {
@@ -1806,22 +1843,24 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
         const uint32_t nb = r[0];
         bool ok = true;
         float y = cc;
-        for (uint32_t k = 0; k <= nb && ok; ++k) {
+        for (uint32_t k = 0; k <= nb; ++k) {
           const uint32_t sb = r[1u + 3u * k];
-          if (sb != kEmptyRun) {
-            const uint32_t cb = __float_as_uint(y);
-            const uint32_t inc = (cb & 1u) ? r[3u + 3u * k] : r[2u + 3u * k];
-            const uint32_t nbits = cb + inc;
-            if ((cb & 0xff800000u) != sb || inc >= kSat || nbits >= sb + 0x00800000u) {
-              ok = false;
-              break;
-            }
-            y = __uint_as_float(nbits);
+          const uint32_t cb = __float_as_uint(y);
+          const uint32_t inc = (cb & 1u) ? r[3u + 3u * k] : r[2u + 3u * k];
+          const uint32_t nbits = cb + inc;
+          const bool run = sb != kEmptyRun;
+          if (run && ((cb & 0xff800000u) != sb || inc >= kSat || nbits >= sb + 0x00800000u)) {
+            ok = false;
+            break;
           }
+          if (run) y = __uint_as_float(nbits);
           if (k == nb) break;
           const float* bx = reinterpret_cast<const float*>(r + 4u + 3u * nb) + k * (uint32_t)M;
+          float xq[M];
 #pragma unroll
-          for (int q = 0; q < M; ++q) y = __fadd_rn(y, bx[q]);
+          for (int q = 0; q < M; ++q) xq[q] = bx[q];
+#pragma unroll
+          for (int q = 0; q < M; ++q) y = __fadd_rn(y, xq[q]);
         }
         if (!ok) break;
         cc = y;
@@ -1840,7 +1879,6 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
     const uint32_t lo = si.lo + (id % kChainMaxQ) * chunk;
     float x[M];
     chain_load<M>(row, si, lo + t * (uint32_t)M, m1, x);
-    LUMEN_TICK(s.misc_size[j] == 0u ? (j == 0 ? "walk_norecord0" : "walk_norecord") : (j == 0 ? "walk_mismatch0" : "walk_mismatch"), b);
     c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
     LUMEN_TICK("walk_recomputed", b);
     j0 = j + 1u;
@@ -1848,10 +1886,36 @@ __device__ __forceinline__ float chain_sum(const KernelArgs& a, int b, uint32_t 
   return c;
 }
 
+// After the row barrier (m1 known): this workgroup's candidates, still in
+// list A as (~key << 32) | id, are rewritten to the row's candidate buffer as
+// (exp(v - m1) bits << 32) | id, and their exp-mass is binned by logit over
+// [tau, m1] into this slice's histogram (used to size the top-p window).
+__device__ __forceinline__ void slice_candidates(const KernelArgs& a, int b, uint32_t sl,
+                                                 uint64_t* cand, uint32_t base, uint32_t n,
+                                                 float m1, uint32_t tau, Smem& s) {
+  const uint32_t t = threadIdx.x;
+  float* hloc = reinterpret_cast<float*>(s.H);
+  for (uint32_t i = t; i < (uint32_t)kMassBins; i += kThreads) hloc[i] = 0.f;
+  __syncthreads();
+  const float tv = tau ? key2f(tau) : kNegInf;
+  const float span = tau ? __fsub_rn(m1, tv) : 0.f;
+  const float inv_w = span > 0.f ? __fdiv_rn((float)kMassBins, span) : 0.f;
+  for (uint32_t j = t; j < n; j += kThreads) {
+    const uint64_t e = s.A[j];
+    const float v = key2f(~(uint32_t)(e >> 32));
+    const float x = expf_glibc(__fsub_rn(v, m1));
+    if (base + j < (uint32_t)kCandCap) cand[base + j] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)e;
+    if (inv_w > 0.f && v >= tv)
+      atomicAdd(&hloc[min((uint32_t)kMassBins - 1u, (uint32_t)(__fsub_rn(m1, v) * inv_w))], x);
+  }
+  __syncthreads();
+  float* hg = a.hist + ((uint64_t)b * kMaxSlices + sl) * kMassBins;
+  for (uint32_t i = t; i < (uint32_t)kMassBins; i += kThreads) hg[i] = hloc[i];
+}
+
 __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b, const RowParams P,
                                                      const Row row, float m1, float S1, uint32_t tau,
-                                                     uint32_t ncand, const uint64_t* cand,
-                                                     float rdraw, Smem& s, RowTrace tr);
+                                                     uint32_t ncand, float rdraw, Smem& s, RowTrace tr);
 
 // Top-p without top-k or penalties. Pass 1 (all slices): slice max, an
 // exp-sum estimate, and the candidates above a sampled logit threshold.
@@ -1865,9 +1929,9 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
-  LUMEN_TICK("p_start", b + (int)sl - (int)(G - 1u));
+  LUMEN_TICK("p_start", b + (int)sl);
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
-  LUMEN_TICK("p_sampled", b + (int)sl - (int)(G - 1u));
+  LUMEN_TICK("p_sampled", b + (int)sl);
   const float tv = tau ? key2f(tau) : kNegInf;
   const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
   float mt = kNegInf;
@@ -1889,6 +1953,8 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     list_push(s.A, &s.cnt, !isn && (tau == 0u || v >= lo_v), ((uint64_t)(~tkey(v)) << 32) | i);
   });
   flush_candidates(cand, &ws.cand_n, s);
+  const uint32_t my_base = s.misc_u[1];
+  const uint32_t my_n = min(s.cnt, (uint32_t)kCap);
   const float ms = block_rmax(mt, s);
   nan = block_or_u32(nan, s);
   double es = (mt == kNegInf) ? 0.0 : et * exp((double)mt - (double)ms);
@@ -1899,12 +1965,12 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     ws.part_nan[sl] = nan;
     ws.part_e[sl] = es_tot;
   }
-  LUMEN_TICK("p_pass1", b + (int)sl - (int)(G - 1u));
+  LUMEN_TICK("p_pass1", b + (int)sl);
   wg_arrive(&ws.bar, s);
   const bool ok = wg_wait_geq(&ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  LUMEN_TICK("p_barrier", b + (int)sl - (int)(G - 1u));
+  LUMEN_TICK("p_barrier", b + (int)sl);
   float m1 = kNegInf;
   uint32_t anynan = 0;
   double p_slice = 0.0;
@@ -1921,26 +1987,63 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const bool single = anynan || !is_finite(m1) || ncand > (uint32_t)kCandCap;
   const bool m16 = sc_len_max(V, G) <= 16u * kThreads;
   uint32_t fits = 0;
-  if (ok && !single)
+  if (ok && !single) {
+    slice_candidates(a, b, sl, cand, my_base, my_n, m1, tau, s);
     fits = m16 ? chain_prepare<16>(a, b, sl, row, sc, m1, p_slice, s)
                : chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
+  }
   if (threadIdx.x == 0) ws.part_fits[sl] = fits;
-  LUMEN_TICK("p_prepared", b + (int)sl - (int)(G - 1u));
-  if (wg_arrive(&ws.arrive, s) != G - 1u) return;
+  LUMEN_TICK("p_prepared", b + (int)sl);
+  if (wg_arrive(&ws.arrive, s) != G - 1u) {
+    LUMEN_TICK("p_not_finisher", b + (int)sl);
+    LUMEN_TICK_DUMP(b + (int)sl);
+    return;
+  }
   LUMEN_TICK("p_finisher", b);
   if (!ok || single ||
       __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
     row_single(a, b, s);
     return;
   }
-  const float S1 = m16 ? chain_sum<16>(a, b, G, row, m1, ws, s) : chain_sum<32>(a, b, G, row, m1, ws, s);
+  // Inputs from the other workgroups, fetched with as few dependent round
+  // trips as possible: the candidates (exp already applied) into list A, the
+  // summed mass histogram into H, then the parked records into list B.
+  {
+    const uint32_t t = threadIdx.x;
+    const uint32_t nc = min(ncand, (uint32_t)kCap);
+    uint64_t c[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t j = (uint32_t)q * kThreads + t;
+      c[q] = j < nc ? cand[j] : 0ull;
+    }
+    float hsum = 0.f;
+    if (t < (uint32_t)kMassBins) {
+      const float* hp = a.hist + (uint64_t)b * kMaxSlices * kMassBins + t;
+      for (uint32_t i = 0; i < G; ++i) hsum += hp[(uint64_t)i * kMassBins];
+    }
+    if (m16) chain_slots<16>(a, b, G, ws, 2u * kCap, s);
+    else chain_slots<32>(a, b, G, ws, 2u * kCap, s);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t j = (uint32_t)q * kThreads + t;
+      if (j < nc) s.A[j] = c[q];
+    }
+    if (t < (uint32_t)kMassBins) reinterpret_cast<float*>(s.H)[t] = hsum;
+    chain_gather_issue(a, b, reinterpret_cast<uint32_t*>(s.Bk), s);
+    __syncthreads();
+  }
+  LUMEN_TICK("p_gathered", b);
+  const uint32_t* recs = reinterpret_cast<const uint32_t*>(s.Bk);
+  const float S1 = m16 ? chain_walk<16>(a, b, G, row, m1, recs, s)
+                       : chain_walk<32>(a, b, G, row, m1, recs, s);
   LUMEN_TICK("p_chain", b);
   RowTrace tr;
   init_trace(tr, V);
   tr.path = 4u;
   tr.passes = 2;
   tr.topp_sum = S1;
-  topp_window(a, b, P, row, m1, S1, tau, ncand, cand, rdraw, s, tr);
+  topp_window(a, b, P, row, m1, S1, tau, ncand, rdraw, s, tr);
 }
 
 // Window 1 of the top-p order: the candidates with p >= p(tau), sorted by
@@ -1949,8 +2052,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
 // hands the row to the exact single-workgroup path.
 __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b, const RowParams P,
                                                      const Row row, float m1, float S1, uint32_t tau,
-                                                     uint32_t ncand, const uint64_t* cand,
-                                                     float rdraw, Smem& s, RowTrace tr) {
+                                                     uint32_t ncand, float rdraw, Smem& s, RowTrace tr) {
   const uint32_t t = threadIdx.x;
   const float tv = tau ? key2f(tau) : kNegInf;
   // The candidates hold every logit >= tau (and a margin below). Their
@@ -1960,58 +2062,11 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
   // tau). The bin masses only steer the window size: the crossing itself is
   // found exactly on the sorted window, and a window that misses it hands
   // the row to the exact path.
-  constexpr uint32_t kBins = 512;
-  float* hmass = reinterpret_cast<float*>(s.H);
-  // one histogram per wave (in the list area B, free until the window is
-  // built), so that atomics only collide inside a wave
-  float* hwave = reinterpret_cast<float*>(s.Bk) + (t >> 6) * kBins;
+  constexpr uint32_t kBins = (uint32_t)kMassBins;
+  const float* hmass = reinterpret_cast<const float*>(s.H);
   const float span = tau ? __fsub_rn(m1, tv) : 0.f;
   const bool binned = tau && span > 0.f;
-  const float inv_w = binned ? __fdiv_rn((float)kBins, span) : 0.f;
-  for (uint32_t i = t; i < kBins * (uint32_t)kWaves; i += kThreads)
-    reinterpret_cast<float*>(s.Bk)[i] = 0.f;
-  __syncthreads();
-  // stage the candidates in LDS as (exp(v - m1) bits << 32) | index, all
-  // loads in flight together; bin the exp-mass of those >= tau
   const uint32_t nc = min(ncand, (uint32_t)kCap);
-  for (uint32_t base = 0; base < nc; base += 8u * kThreads) {
-    uint64_t c[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t j = base + (uint32_t)q * kThreads + t;
-      c[q] = j < nc ? cand[j] : 0ull;
-    }
-#ifdef LUMEN_TIMING
-    {
-      uint64_t acc = 0;
-      for (int q = 0; q < 8; ++q) acc ^= c[q];
-      if (acc == 0x123456789ull) s.misc_u[0] = 1;
-      __syncthreads();
-      LUMEN_TICK("p_cand_loaded", b);
-    }
-#endif
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t j = base + (uint32_t)q * kThreads + t;
-      if (j < nc) {
-        const float v = key2f(~(uint32_t)(c[q] >> 32));
-        const float x = expf_glibc(__fsub_rn(v, m1));
-        s.A[j] = ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)c[q];
-        if (binned && v >= tv)
-          atomicAdd(&hwave[min(kBins - 1u, (uint32_t)(__fsub_rn(m1, v) * inv_w))], x);
-      }
-    }
-  }
-  __syncthreads();
-  LUMEN_TICK("p_cand_binned", b);
-  for (uint32_t i = t; i < kBins; i += kThreads) {
-    float m = 0.f;
-#pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) m += reinterpret_cast<const float*>(s.Bk)[wv * kBins + i];
-    hmass[i] = m;
-  }
-  __syncthreads();
-  LUMEN_TICK("p_staged", b);
   float v_thr = tv;
   if (binned) {
     // first bin (from the top) where the running mass reaches the target
@@ -2055,7 +2110,13 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
   __syncthreads();
   const uint32_t n = s.cnt;
   LUMEN_TICK("p_window_built", b);
-  sort_u64_asc(s.Bk, n, s.A, s);
+  {
+    // keys (~p bits << 32) | id with p in [p_lo, 1/S1]: their common high
+    // bits are known without a reduction
+    const uint32_t khi = ~__float_as_uint(__fdiv_rn(1.0f, S1)), klo = ~__float_as_uint(p_lo);
+    const uint64_t hint = p_lo > 0.f ? ((uint64_t)(khi ^ klo) << 32) | span_mask(a.vocab) : 0ull;
+    sort_u64_asc(s.Bk, n, s.A, s, hint);
+  }
   LUMEN_TICK("p_window_sorted", b);
   EcssResult wk = list_ecss(
       n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe,
@@ -2074,9 +2135,10 @@ __device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b
     s.A[j] = ((uint64_t)idx << 32) | tkey(row.at(idx));
   }
   __syncthreads();
-  sort_u64_asc(s.A, nk, s.Bk, s);
+  sort_u64_asc(s.A, nk, s.Bk, s, ((uint64_t)span_mask(a.vocab) << 32) | 0xffffffffull);
   LUMEN_TICK("p_kept_sorted", b);
-  small_path(a, b, P, nk, true, rdraw, s, tr);
+  // the kept set holds the row maximum m1
+  small_path(a, b, P, nk, true, rdraw, s, tr, m1);
 }
 
 // Row and slice of this workgroup. With xcd_rows, blocks are dispatched to
@@ -2121,7 +2183,6 @@ __device__ __attribute__((noinline)) void row_exit(const KernelArgs& a, Smem& s)
     ws.bar = 0;
     ws.cand_n = 0;
     ws.status = 0;
-    for (uint32_t i = 0; i < G; ++i) ws.chain_flag[i] = 0;
     __threadfence();
     ws.exit_ = 0;
     __threadfence();
