@@ -67,9 +67,9 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
   uint32_t fixed = 0;
   for (uint32_t b = 0; b < B; ++b) {
     switch (row_path(rows[b], V, lumen::kMaxSlices)) {
-      case kPathGreedy: w[b] = 2; break;
-      case kPathTopK: w[b] = 3; break;
-      case kPathTopP: w[b] = 6; break;
+      case kPathGreedy: w[b] = 1; break;
+      case kPathTopK: w[b] = 2; break;
+      case kPathTopP: w[b] = 10; break;
       default: w[b] = 0; ++fixed; break;  // exact single-workgroup row
     }
     wsum += w[b];

@@ -679,22 +679,49 @@ __device__ __forceinline__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, 
 
 template <class X>
 __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
-  if (n <= (uint32_t)kEstBx) {
+  if (n <= 128u) {
     // short lists: the summands go to LDS in parallel and one thread adds
-    // them in order, which is the reference's own loop
+    // them in order, which is the reference's own loop (a dependent f32 add
+    // costs ~20 ns here, so this only pays for short lists)
     float* xs = s.est.bx;
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = xf(j);
     __syncthreads();
     if (threadIdx.x == 0) {
+      // blocks of 16: the adds are the only dependent chain; the search
+      // test runs on the block's partial sums afterwards
       float c = c0, prev = c0;
       int pos = -1;
-      for (uint32_t j = 0; j < n; ++j) {
-        prev = c;
-        c = __fadd_rn(c, xs[j]);
-        if (mode != kEcssSum && ecss_cond(mode, c, theta)) {
-          pos = (int)j;
-          break;
+      for (uint32_t j0 = 0; j0 < n && pos < 0; j0 += 16u) {
+        float xv[16], cs[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) xv[q] = (j0 + (uint32_t)q < n) ? xs[j0 + q] : 0.f;
+        float y = c;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          y = __fadd_rn(y, xv[q]);
+          cs[q] = y;
         }
+        // the running sum never decreases: a block without a hit at its end
+        // has none inside (padding adds zeros)
+        if (mode != kEcssSum && ecss_cond(mode, y, theta)) {
+          int hq = 16;
+#pragma unroll
+          for (int q = 15; q >= 0; --q)
+            if (j0 + (uint32_t)q < n && ecss_cond(mode, cs[q], theta)) hq = q;
+          if (hq < 16) {
+            pos = (int)j0 + hq;
+            float pb = c;
+#pragma unroll
+            for (int q = 1; q < 16; ++q) pb = (q == hq) ? cs[q - 1] : pb;
+            float yh = cs[0];
+#pragma unroll
+            for (int q = 1; q < 16; ++q) yh = (q == hq) ? cs[q] : yh;
+            prev = pb;
+            c = yh;
+            break;
+          }
+        }
+        c = y;
       }
       s.est.c_out = c;
       s.est.before = prev;
