@@ -397,7 +397,7 @@ __device__ __forceinline__ void radix_pass(const uint64_t* src, uint64_t* dst, u
 // (both in LDS). Only the bits in which the keys differ are sorted, in 8-bit
 // digits starting at the lowest differing bit, so the cost is about one read
 // and one write of the list per 8 varying bits.
-__device__ __attribute__((noinline)) void radix_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n, Smem& s) {
+__device__ __forceinline__ void radix_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n, Smem& s) {
   const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
   uint64_t o = 0ull, an = ~0ull;
   for (uint32_t j = t; j < n; j += kThreads) {
@@ -514,7 +514,7 @@ constexpr uint32_t kBucketMax = 256;  // largest bucket ranked by direct countin
 // bucket that sort before it, which gives its final position whatever
 // order the atomic scatter left inside the bucket. When a bucket holds
 // more than kBucketMax keys the radix sort takes over.
-__device__ __attribute__((noinline)) void bucket_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n,
+__device__ __forceinline__ void bucket_sort_u64(uint64_t* a, uint64_t* tmp, uint32_t n,
                                                           uint64_t diff_hint, Smem& s) {
   const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
   uint64_t diff = diff_hint;  // a superset of the bits in which keys differ, or 0
@@ -820,7 +820,7 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
 // n entries, every entry alive). Applies min-p, temperature, softmax, draw.
 // known_max: the largest logit of the list when the caller knows it (the
 // list is NaN-free then), NaN otherwise.
-__device__ __attribute__((noinline)) uint32_t final_on_list(const KernelArgs& a, const RowParams P, uint32_t n, float r,
+__device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const RowParams P, uint32_t n, float r,
                                   Smem& s, RowTrace& tr, float known_max) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
@@ -1940,7 +1940,7 @@ __device__ __forceinline__ void slice_candidates(const KernelArgs& a, int b, uin
   for (uint32_t i = t; i < (uint32_t)kMassBins; i += kThreads) hg[i] = hloc[i];
 }
 
-__device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b, const RowParams P,
+__device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const RowParams P,
                                                      const Row row, float m1, float S1, uint32_t tau,
                                                      uint32_t ncand, float rdraw, Smem& s, RowTrace tr);
 
@@ -2077,7 +2077,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
 // (p desc, index asc), walked with the exact cumulative sum; the kept prefix
 // continues on the small path in index order. A crossing outside the window
 // hands the row to the exact single-workgroup path.
-__device__ __attribute__((noinline)) void topp_window(const KernelArgs& a, int b, const RowParams P,
+__device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const RowParams P,
                                                      const Row row, float m1, float S1, uint32_t tau,
                                                      uint32_t ncand, float rdraw, Smem& s, RowTrace tr) {
   const uint32_t t = threadIdx.x;
@@ -2200,7 +2200,7 @@ __device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint
 // The last workgroup of a row to leave restores its coordination block. The
 // row is derived again from the block index, so nothing has to stay live
 // across the path calls.
-__device__ __attribute__((noinline)) void row_exit(const KernelArgs& a, Smem& s) {
+__device__ __forceinline__ void row_exit(const KernelArgs& a, Smem& s) {
   uint32_t b, sl, G;
   block_row(a, b, sl, G);
   RowWs& ws = a.ws[b];
