@@ -220,6 +220,81 @@ __device__ __forceinline__ EcssResult ecss_chunk(float c, const float (&x)[M], i
 }
 
 // ---------------------------------------------------------------------------
+// One-wave variant for short lists: lane l holds elements l*M .. l*M+M-1.
+// The same parity-map method with a DPP wave scan instead of a block scan,
+// so a binade crossing costs one wave scan and no workgroup barrier. Must
+// be called by all 64 lanes of one wave; the result is uniform across it.
+template <int M>
+__device__ __forceinline__ EcssResult wave_ecss(float c, const float (&x)[M], int mode, float theta) {
+  const int lane = threadIdx.x & 63;
+  int t0 = 0;
+  EcssResult res;
+  for (;;) {
+    const uint32_t cb = __float_as_uint(c);
+    const uint32_t b0 = cb & 0xff800000u;
+    const uint32_t ub = b0 + 0x00800000u;
+    PMap m{0u, 0u};
+    if (lane >= t0) {
+      float y0 = __uint_as_float(b0), y1 = __uint_as_float(b0 | 1u);
+#pragma unroll
+      for (int j = 0; j < M; ++j) {
+        y0 = __fadd_rn(y0, x[j]);
+        y1 = __fadd_rn(y1, x[j]);
+      }
+      const uint32_t n0 = __float_as_uint(y0) - b0, n1 = __float_as_uint(y1) - (b0 | 1u);
+      m.a0 = n0 > kSat ? kSat : n0;
+      m.a1 = n1 > kSat ? kSat : n1;
+    }
+    const PMap id{0u, 0u};
+    const PMap ex = wave_shr1(wave_scan_incl(m, id, pm_combine), id);
+    const uint32_t par0 = cb & 1u;
+    const uint32_t before = par0 ? ex.a1 : ex.a0;
+    const uint32_t own = ((par0 ^ before) & 1u) ? m.a1 : m.a0;
+    const uint32_t sbits = cb + before;
+    const uint32_t ebits = sbits + own;
+    const bool act = lane >= t0;
+    const bool cross = act && (before >= kSat || ebits >= ub);
+    const bool hit = act && !cross && mode != kEcssSum && ecss_cond(mode, __uint_as_float(ebits), theta);
+    const unsigned long long bm = __ballot(cross), hm = __ballot(hit);
+    const int tb = bm ? __ffsll((long long)bm) - 1 : 64;
+    const int th = hm ? __ffsll((long long)hm) - 1 : 64;
+    if (th < tb || tb < 64) {
+      // lane r (the hit, or the crossing) replays its elements from its exact start
+      const int r = th < tb ? th : tb;
+      float y = __uint_as_float(sbits), prev = y;
+      int j = M;
+#pragma unroll
+      for (int q = 0; q < M; ++q) {
+        if (j == M) {
+          prev = y;
+          y = __fadd_rn(y, x[q]);
+          if (mode != kEcssSum && ecss_cond(mode, y, theta)) j = q;
+        }
+      }
+      const int jr = __builtin_amdgcn_readlane(j, r);
+      const float yr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(y), r));
+      if (jr < M) {
+        res.c = yr;
+        res.found = 1;
+        res.pos = r * M + jr;
+        res.before = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(prev), r));
+        return res;
+      }
+      c = yr;
+      t0 = r + 1;
+      if (t0 < 64) continue;
+      res.c = c;
+    } else {
+      res.c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)ebits, 63));
+    }
+    res.found = 0;
+    res.pos = -1;
+    res.before = 0.f;
+    return res;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Estimate-guided variant: no block scan per binade crossing.
 //
 // ecss_chunk pays one block scan each time the running sum changes binade,

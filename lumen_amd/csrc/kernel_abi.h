@@ -61,7 +61,8 @@ constexpr uint32_t kIdleBlock = 0xffffffffu;
 constexpr int kCandCap = 8192;
 constexpr int kMassBins = 512;       // top-p window planning bins      // per-row candidate buffer (entries)
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
-constexpr int kEstSharedBytes = 8192;  // upper bound of one parked run structure
+constexpr int kRowRecs = kMaxSlices * kChainMaxQ * 16;  // run records per row (one per wave segment)
+constexpr int kRecWords = 1152;     // words per run record slot
 
 // Per-row coordination block in device memory. Zero at allocation; the last
 // workgroup of a row to finish restores the counters to zero, so every
@@ -73,12 +74,10 @@ struct RowWs {
   uint32_t cand_n;       // candidates appended
   uint32_t status;       // row failure bits
   uint32_t pad[3];
-  uint32_t part_words[kMaxSlices * kChainMaxQ];  // parked record sizes (32-bit words)
   float part_max[kMaxSlices];
   uint32_t part_nan[kMaxSlices];
   uint64_t part_arg[kMaxSlices];
   double part_e[kMaxSlices];
-  uint32_t part_fits[kMaxSlices];  // bit q: sub-chunk q's run structure is parked
 };
 
 struct KernelArgs {
@@ -101,8 +100,7 @@ struct KernelArgs {
   // Small batches pass their parameters and draws inside the kernel
   // arguments (no staging copy): used when inline_rows > 0.
   RowWs* ws;                 // [B] coordination blocks
-  uint32_t* est;             // [B][kMaxSlices][kChainMaxQ] parked run structures
-                             // (kEstSharedBytes each)
+  uint32_t* est;             // [B][kRowRecs][kRecWords] run records of wave segments
   uint64_t* cand;            // [B][kCandCap] candidate buffers
   float* hist;               // [B][kMaxSlices][kMassBins] candidate exp-mass per logit bin
   uint32_t slices;           // workgroups per row (G) when blk_map is NULL

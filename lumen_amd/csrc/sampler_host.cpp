@@ -125,7 +125,7 @@ struct lumen_sampler {
   DevBuf pen_scratch;
   DevBuf ws;    // [B] RowWs, zeroed at allocation, self-resetting afterwards
   DevBuf cand;  // [B][kCandCap] candidate buffers
-  DevBuf est;   // [B][kMaxSlices][kChainMaxQ] parked run structures
+  DevBuf est;   // [B][kRowRecs][kRecWords] run records of the split top-p path
   DevBuf hist;  // [B][kMaxSlices][kMassBins] candidate mass histograms
   int cu_count = 0;
   int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
@@ -539,8 +539,7 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
     }
     int rc = ensure_dev(s->cand, sizeof(uint64_t) * lumen::kCandCap * B);
     if (rc != LUMEN_OK) return rc;
-    rc = ensure_dev(s->est, (size_t)lumen::kEstSharedBytes * lumen::kMaxSlices *
-                                lumen::kChainMaxQ * B);
+    rc = ensure_dev(s->est, sizeof(uint32_t) * lumen::kRecWords * lumen::kRowRecs * B);
     if (rc != LUMEN_OK) return rc;
     ka.ws = static_cast<lumen::RowWs*>(s->ws.p);
     ka.cand = static_cast<uint64_t*>(s->cand.p);

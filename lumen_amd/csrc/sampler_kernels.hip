@@ -39,19 +39,26 @@
 // once when that row's result is written.
 #ifdef LUMEN_TIMING
 #include <cstdio>
-__shared__ unsigned long long g_ticks[26];
-__shared__ const char* g_tick_names[26];
+// one log per slice of row 0 in device memory; the workgroup's log index
+// (or -1) sits in LDS
+__device__ unsigned long long g_tick_t[16][64];
+__device__ const char* g_tick_l[16][64];
+__shared__ int g_tick_slot;
 __shared__ int g_nticks;
-#define LUMEN_TICK(label, b)                                         \
-  do {                                                              \
-    if (threadIdx.x == 0 && (b) == 0 && g_nticks < 26) {            \
-      g_ticks[g_nticks] = wall_clock64();                           \
-      g_tick_names[g_nticks++] = label;                             \
-    }                                                               \
+#define LUMEN_TICK(label, b)                                                   \
+  do {                                                                        \
+    if (threadIdx.x == 0 && (b) == 0 && g_tick_slot >= 0 && g_nticks < 64) {  \
+      g_tick_t[g_tick_slot][g_nticks] = wall_clock64();                       \
+      g_tick_l[g_tick_slot][g_nticks++] = label;                              \
+    }                                                                         \
   } while (0)
 #define LUMEN_TICK_INIT() \
   do {                    \
-    if (threadIdx.x == 0) g_nticks = 0; \
+    if (threadIdx.x == 0) { g_nticks = 0; g_tick_slot = -1; } \
+  } while (0)
+#define LUMEN_TICK_SLOT(row, sl) \
+  do {                           \
+    if (threadIdx.x == 0) g_tick_slot = ((row) == 0 && (sl) < 16) ? (int)(sl) : -1; \
   } while (0)
 #define LUMEN_TICK_RESET(b) \
   do {                      \
@@ -59,14 +66,15 @@ __shared__ int g_nticks;
   } while (0)
 #define LUMEN_TICK_DUMP(b)                                                       \
   do {                                                                          \
-    if (threadIdx.x == 0 && (b) == 0)                                           \
+    if (threadIdx.x == 0 && (b) == 0 && g_tick_slot >= 0)                       \
       for (int i_ = 1; i_ < g_nticks; ++i_)                                     \
-        printf("tick %s +%f us\n", g_tick_names[i_],                       \
-               (double)(g_ticks[i_] - g_ticks[i_ - 1]) / 100.0);                \
+        printf("tick[%d] %s +%f us\n", g_tick_slot, g_tick_l[g_tick_slot][i_],  \
+               (double)(g_tick_t[g_tick_slot][i_] - g_tick_t[g_tick_slot][i_ - 1]) / 100.0); \
   } while (0)
 #else
 #define LUMEN_TICK(label, b) do { } while (0)
 #define LUMEN_TICK_INIT() do { } while (0)
+#define LUMEN_TICK_SLOT(row, sl) do { } while (0)
 #define LUMEN_TICK_RESET(b) do { } while (0)
 #define LUMEN_TICK_DUMP(b) do { } while (0)
 #endif
@@ -76,7 +84,6 @@ __shared__ int g_nticks;
 namespace lumen {
 
 constexpr int kCap = 8192;          // LDS list capacity (entries)
-constexpr int kSlots = kMaxSlices * kChainMaxQ;  // parked run records per row
 constexpr int kCapWindow = kCap - 512;  // planned window size (margin for equal-probability spill)
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -94,8 +101,6 @@ struct Smem {
   uint32_t cnt;
   int misc_i[4];
   uint32_t misc_u[4];
-  uint32_t misc_slot[2 * kSlots];  // chained-sum record offsets and slot ids
-  uint32_t misc_size[kSlots];
 };
 
 // ---------------------------------------------------------------- helpers
@@ -677,55 +682,31 @@ __device__ __forceinline__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, 
   return ecss_fast_chunk<M>(c0, x, mode, theta, s.ecss, s.est, s.wsum, (int)min((uint32_t)kThreads, (n + (uint32_t)M - 1u) / (uint32_t)M));
 }
 
+// The one-wave method on a list of n <= 64 * M elements (wave 0 only).
+template <int M, class X>
+__device__ __forceinline__ EcssResult list_ecss_wave(uint32_t n, X&& xf, int mode, float theta, float c0) {
+  const uint32_t j0 = (threadIdx.x & 63u) * M;
+  float x[M];
+#pragma unroll
+  for (int q = 0; q < M; ++q) x[q] = (j0 + q < n) ? xf(j0 + q) : 0.f;
+  return wave_ecss<M>(c0, x, mode, theta);
+}
+
 template <class X>
 __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
-  if (n <= 128u) {
-    // short lists: the summands go to LDS in parallel and one thread adds
-    // them in order, which is the reference's own loop (a dependent f32 add
-    // costs ~20 ns here, so this only pays for short lists)
-    float* xs = s.est.bx;
-    for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = xf(j);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      // blocks of 16: the adds are the only dependent chain; the search
-      // test runs on the block's partial sums afterwards
-      float c = c0, prev = c0;
-      int pos = -1;
-      for (uint32_t j0 = 0; j0 < n && pos < 0; j0 += 16u) {
-        float xv[16], cs[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) xv[q] = (j0 + (uint32_t)q < n) ? xs[j0 + q] : 0.f;
-        float y = c;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          y = __fadd_rn(y, xv[q]);
-          cs[q] = y;
-        }
-        // the running sum never decreases: a block without a hit at its end
-        // has none inside (padding adds zeros)
-        if (mode != kEcssSum && ecss_cond(mode, y, theta)) {
-          int hq = 16;
-#pragma unroll
-          for (int q = 15; q >= 0; --q)
-            if (j0 + (uint32_t)q < n && ecss_cond(mode, cs[q], theta)) hq = q;
-          if (hq < 16) {
-            pos = (int)j0 + hq;
-            float pb = c;
-#pragma unroll
-            for (int q = 1; q < 16; ++q) pb = (q == hq) ? cs[q - 1] : pb;
-            float yh = cs[0];
-#pragma unroll
-            for (int q = 1; q < 16; ++q) yh = (q == hq) ? cs[q] : yh;
-            prev = pb;
-            c = yh;
-            break;
-          }
-        }
-        c = y;
+  if (n <= 64u * 32u) {
+    // short lists: one wave, no workgroup barrier inside
+    if (threadIdx.x < 64u) {
+      EcssResult r;
+      if (n <= 64u * 2u) r = list_ecss_wave<2>(n, xf, mode, theta, c0);
+      else if (n <= 64u * 8u) r = list_ecss_wave<8>(n, xf, mode, theta, c0);
+      else r = list_ecss_wave<32>(n, xf, mode, theta, c0);
+      if (threadIdx.x == 0) {
+        s.est.c_out = r.c;
+        s.est.before = r.before;
+        s.est.hit_pos = r.found ? r.pos : -1;
+        s.est.fail = 0;
       }
-      s.est.c_out = c;
-      s.est.before = prev;
-      s.est.hit_pos = pos;
     }
     __syncthreads();
     EcssResult e;
@@ -884,14 +865,18 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
     tr.cdf_before = tr.cdf_at = __uint_as_float(0x7fc00000u);
     return V - 1;
   }
-  EcssResult S = list_ecss(n, [&](uint32_t j) { return expf_glibc(__fsub_rn(wv(j), m3)); },
-                           kEcssSum, 0.f, 0.f, s);
+  // the summands, then the probabilities, computed by the whole workgroup
+  // into LDS (list B is free here); the exact sums read them back
+  float* xs = reinterpret_cast<float*>(s.Bk);
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = expf_glibc(__fsub_rn(wv(j), m3));
+  __syncthreads();
+  EcssResult S = list_ecss(n, [&](uint32_t j) { return xs[j]; }, kEcssSum, 0.f, 0.f, s);
   const float S3 = S.c;
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
+  __syncthreads();
   LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", 0);
   tr.final_sum = S3;
-  EcssResult e = list_ecss(
-      n, [&](uint32_t j) { return __fdiv_rn(expf_glibc(__fsub_rn(wv(j), m3)), S3); },
-      kEcssFindGt, r, 0.f, s);
+  EcssResult e = list_ecss(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
   LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", 0);
   LUMEN_TICK("fin_walk", 0);
   tr.cdf_before = e.found ? e.before : e.c;
@@ -1593,9 +1578,9 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
-  LUMEN_TICK("topk_start", b + (int)sl);
+  LUMEN_TICK("topk_start", b);
   const uint32_t tau = sample_threshold(row, V, target, s);
-  LUMEN_TICK("topk_sampled", b + (int)sl);
+  LUMEN_TICK("topk_sampled", b);
   const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
   if (threadIdx.x == 0) s.cnt = 0;
   __syncthreads();
@@ -1621,7 +1606,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     }
   }
   flush_candidates(cand, &ws.cand_n, s);
-  LUMEN_TICK("topk_compacted", b + (int)sl);
+  LUMEN_TICK("topk_compacted", b);
   const uint32_t old = wg_arrive(&ws.arrive, s);
   if (old != G - 1u) return;
   LUMEN_TICK("topk_finisher", b);
@@ -1713,7 +1698,6 @@ __device__ __forceinline__ uint32_t binade_bits(double x) {
 // then walks all structures in row order (est_resolve), exactly; a
 // sub-chunk whose structure failed a check is recomputed and summed by the
 // iterative method instead.
-static_assert(sizeof(EstShared) <= (size_t)kEstSharedBytes, "parked run structure too large");
 
 template <int M>
 __device__ __forceinline__ void chain_load(const Row& row, Slice sc, uint32_t i0, float m1,
@@ -1728,43 +1712,154 @@ __device__ __forceinline__ void chain_load(const Row& row, Slice sc, uint32_t i0
   }
 }
 
-__device__ __forceinline__ uint32_t* est_slot(const KernelArgs& a, int b, uint32_t sl, uint32_t q) {
-  return a.est + (((uint64_t)b * kMaxSlices + sl) * kChainMaxQ + q) * (kEstSharedBytes / 4);
-}
-
-
-// A run structure is parked as a compact record of 32-bit words:
-//   [0]                    nb (boundary threads)
+// ---------------------------------------------------------------- records
+// Run records of the exact softmax sum, one per wave segment. In pass 2 a
+// sub-chunk of kThreads * M elements gives thread t elements t M .. t M + M
+// - 1, so wave w holds a segment of 64 M consecutive elements. Each wave
+// parks that segment's record (the parity-map method of ecss.h at wave
+// scope, guided by the f64 estimate of the running sum):
+//   [0]                    nb (boundary lanes), or kRecNotParked
 //   [1 + 3k .. 3 + 3k]     run k (k = 0..nb): binade bits, map a0, map a1
-//   [4 + 3nb ..]           the M summands of every boundary thread, in order
+//   [4 + 3nb ..]           the M summands of every boundary lane, in order
+// A lane is a boundary when its estimated running sum, widened by `rel`,
+// touches two binades; every other lane builds its parity map in its
+// binade, and a segmented wave scan composes the runs between boundaries.
+// Records with more than kRecMaxB boundary lanes are not parked; the walk
+// sums such a segment again on one wave.
+constexpr uint32_t kRecMaxB = 32;
+constexpr uint32_t kRecNotParked = 0xffffffffu;
+constexpr uint32_t kRecSlots = (uint32_t)kMaxSlices * (uint32_t)kChainMaxQ * (uint32_t)kWaves;
+static_assert(kRecSlots == (uint32_t)kRowRecs, "record slots per row");
+static_assert(4u + 35u * kRecMaxB <= (uint32_t)kRecWords, "record slot too small");
+
 template <int M>
-__device__ __forceinline__ uint32_t record_words(uint32_t nb) {
-  return 1u + 3u * (nb + 1u) + nb * (uint32_t)M;
+__device__ __forceinline__ uint32_t rec_words(uint32_t nb) {
+  return 4u + (3u + (uint32_t)M) * nb;
+}
+
+__device__ __forceinline__ uint32_t* rec_slot(const KernelArgs& a, int b, uint32_t slot) {
+  return a.est + ((uint64_t)b * kRowRecs + slot) * kRecWords;
 }
 
 template <int M>
-__device__ __forceinline__ void park_record(uint32_t* dst, const EstShared& es) {
-  const uint32_t t = threadIdx.x, nb = (uint32_t)es.nb;
-  if (t == 0) dst[0] = nb;
-  if (t <= nb) {
-    dst[1u + 3u * t] = es.seg_bin[t];
-    dst[2u + 3u * t] = es.seg_tot[t].a0;
-    dst[3u + 3u * t] = es.seg_tot[t].a1;
+__device__ __forceinline__ void wave_park(const float (&x)[M], double p_start, double d_self,
+                                          double rel, uint32_t nact, uint32_t* rec) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const bool live = lane < nact;
+  const uint32_t blo = est_binade(p_start * (1.0 - rel));
+  const uint32_t bhi = est_binade((p_start + d_self) * (1.0 + rel));
+  const bool bd = live && blo != bhi;
+  const unsigned long long bm = __ballot(bd);
+  const uint32_t nb = (uint32_t)__popcll(bm);
+  if (nb > kRecMaxB) {
+    if (lane == 0) rec[0] = kRecNotParked;
+    return;
   }
-  const uint32_t* bx = reinterpret_cast<const uint32_t*>(es.bx);
-  for (uint32_t i = t; i < nb * (uint32_t)M; i += kThreads) dst[4u + 3u * nb + i] = bx[i];
+  PMap own{0u, 0u};
+  if (live && !bd) {
+    float y0 = __uint_as_float(blo), y1 = __uint_as_float(blo | 1u);
+#pragma unroll
+    for (int j = 0; j < M; ++j) {
+      y0 = __fadd_rn(y0, x[j]);
+      y1 = __fadd_rn(y1, x[j]);
+    }
+    const uint32_t n0 = __float_as_uint(y0) - blo, n1 = __float_as_uint(y1) - (blo | 1u);
+    own.a0 = n0 > kSat ? kSat : n0;
+    own.a1 = n1 > kSat ? kSat : n1;
+  }
+  const uint32_t k = (uint32_t)__popcll(bm & ((1ull << lane) - 1ull));
+  const SegVal id{0u, PMap{0u, 0u}};
+  const SegVal inc = wave_scan_incl(SegVal{bd ? 1u : 0u, own}, id, seg_combine);
+  const SegVal prev = wave_shr1(inc, id);
+  const uint32_t pbd = wave_shr1(bd ? 1u : 0u, 0u);
+  const uint32_t pbin = wave_shr1(blo, 0u);
+  if (bd) {
+    const bool empty = lane == 0u || pbd != 0u;
+    rec[1u + 3u * k] = empty ? kEmptyRun : pbin;
+    rec[2u + 3u * k] = empty ? 0u : prev.m.a0;
+    rec[3u + 3u * k] = empty ? 0u : prev.m.a1;
+    uint32_t* bx = rec + 4u + 3u * nb + k * (uint32_t)M;
+#pragma unroll
+    for (int j = 0; j < M; ++j) bx[j] = __float_as_uint(x[j]);
+  }
+  if (lane == nact - 1u) {
+    rec[0] = nb;
+    rec[1u + 3u * nb] = bd ? kEmptyRun : blo;
+    rec[2u + 3u * nb] = bd ? 0u : inc.m.a0;
+    rec[3u + 3u * nb] = bd ? 0u : inc.m.a1;
+  }
+}
+
+// Applies run (sb, a0, a1) to the exact running sum c; false when the sum
+// is not in the run's binade or would leave it (the estimate was wrong).
+__device__ __forceinline__ bool run_apply(float& c, uint32_t sb, uint32_t a0, uint32_t a1) {
+  if (sb == kEmptyRun) return true;
+  const uint32_t cb = __float_as_uint(c);
+  const uint32_t inc = (cb & 1u) ? a1 : a0;
+  const uint32_t nbits = cb + inc;
+  if ((cb & 0xff800000u) != sb || inc >= kSat || nbits >= sb + 0x00800000u) return false;
+  c = __uint_as_float(nbits);
+  return true;
 }
 
 template <int M>
-__device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, uint32_t sl,
-                                                  const Row& row, Slice sc, float m1,
-                                                  double p_slice, Smem& s) {
+__device__ __forceinline__ bool rec_walk(const uint32_t* rec, float& c) {
+  const uint32_t nb = rec[0];
+  float y = c;
+  for (uint32_t k = 0; k <= nb; ++k) {
+    if (!run_apply(y, rec[1u + 3u * k], rec[2u + 3u * k], rec[3u + 3u * k])) return false;
+    if (k < nb) {
+      const uint32_t* bx = rec + 4u + 3u * nb + (uint32_t)M * k;
+      float xs[M];
+#pragma unroll
+      for (int q = 0; q < M; ++q) xs[q] = __uint_as_float(bx[q]);
+#pragma unroll
+      for (int q = 0; q < M; ++q) y = __fadd_rn(y, xs[q]);
+    }
+  }
+  c = y;
+  return true;
+}
+
+// Row range of record slot `slot` = (slice, sub-chunk, wave); empty when the
+// segment lies beyond its slice.
+template <int M>
+__device__ __forceinline__ Slice rec_range(uint32_t V, uint32_t G, uint32_t slot) {
+  const uint32_t w = slot % (uint32_t)kWaves, sq = slot / (uint32_t)kWaves;
+  const Slice si = slice_bounds(V, G, sq / (uint32_t)kChainMaxQ);
+  const uint32_t lo = si.lo + (sq % (uint32_t)kChainMaxQ) * (uint32_t)kThreads * M + w * 64u * M;
+  return Slice{min(lo, si.hi), min(si.hi, lo + 64u * M)};
+}
+
+// Exact sum of one segment from the exact running sum c, by the calling wave.
+template <int M>
+__device__ __forceinline__ float seg_recompute(const Row& row, Slice r, float m1, float c) {
+  const uint32_t i0 = r.lo + (threadIdx.x & 63u) * M;
+  float x[M];
+#pragma unroll
+  for (int q = 0; q < M / 4; ++q) {
+    float v[4] = {kNegInf, kNegInf, kNegInf, kNegInf};
+    const uint32_t i = i0 + 4u * q;
+    if (i < r.hi) row.load4(i, v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < r.hi) ? expf_glibc(__fsub_rn(v[j], m1)) : 0.f;
+  }
+  return wave_ecss<M>(c, x, kEcssSum, 0.f).c;
+}
+
+// Pass 2 of a top-p row: the exact summands exp(v - m1) of this slice, per
+// sub-chunk, with one record per wave segment. The incoming sum of the
+// slice is the f64 estimate p_slice.
+template <int M>
+__device__ __forceinline__ void chain_prepare(const KernelArgs& a, int b, uint32_t sl,
+                                              const Row& row, Slice sc, float m1,
+                                              double p_slice, Smem& s) {
   const uint32_t chunk = (uint32_t)kThreads * M;
   const uint32_t nq = (sc.hi - sc.lo + chunk - 1u) / chunk;
-  uint32_t fits = 0;
+  const uint32_t t = threadIdx.x, w = t >> 6;
   double pre = p_slice;
   for (uint32_t q = 0; q < nq; ++q) {
-    const uint32_t i0 = sc.lo + q * chunk + (uint32_t)threadIdx.x * M;
+    const uint32_t i0 = sc.lo + q * chunk + t * M;
     float x[M];
     chain_load<M>(row, sc, i0, m1, x);
     double d = 0.0;
@@ -1773,144 +1868,180 @@ __device__ __forceinline__ uint32_t chain_prepare(const KernelArgs& a, int b, ui
     double tot;
     const double pt = pre + block_excl_scan_f64(d, s, &tot);
     pre += tot;
-    // The incoming sum is only estimated here (other slices' exp-sums); the
-    // rounding drift of a long f32 sum is typically ~1e-5 relative. A wrong
-    // guess only costs the exact recomputation in chain_walk.
     // The exact f32 running sum drifts below its f64 estimate: addends are
     // rounded onto the accumulator's grid, and the small ones are lost. The
     // drift reaches ~5e-4 relative after 250K summands in logit rows, so the
-    // boundary margin grows with the position in the row.
+    // boundary margin grows with the position in the row. A wrong guess
+    // only costs one wave's recomputation in the walk.
     const double rel = 4e-5 + 3e-9 * (double)(sc.lo + q * chunk);
-    EstThread et;
-    if (est_prepare<M>(x, pt, d, rel, s.ecss, s.est, et,
-                       (int)min((uint32_t)kThreads, ((sc.hi - (sc.lo + q * chunk)) + (uint32_t)M - 1u) / (uint32_t)M))) {
-      fits |= 1u << q;
-      park_record<M>(est_slot(a, b, sl, q), s.est);
-      if (threadIdx.x == 0)
-        a.ws[b].part_words[sl * kChainMaxQ + q] = record_words<M>((uint32_t)s.est.nb);
+    const uint32_t nthr = (sc.hi - (sc.lo + q * chunk) + (uint32_t)M - 1u) / (uint32_t)M;
+#ifdef LUMEN_DEBUG_RECORDS
+    if (b == 0 && (t & 63u) == 0 && w * 64u < nthr) {
+      const double pw = wave_read(pt, 0);
+      (void)pw;
     }
-    __syncthreads();
+#endif
+    if (w * 64u < nthr)
+      wave_park<M>(x, pt, d, rel, min(64u, nthr - w * 64u),
+                   rec_slot(a, b, (sl * (uint32_t)kChainMaxQ + q) * (uint32_t)kWaves + w));
   }
-  return fits;
 }
 
-// Exact softmax sum of the row from the parked records (last workgroup of
-// the row). Slots are (slice i, sub-chunk q) in row order; their record
-// sizes come from the coordination block. chain_gather_issue() copies every
-// record into `words` (up to `cap` words) with one bulk copy; chain_walk()
-// then walks runs and boundary summands in order on one wave. A slot without
-// a record, or whose record does not match the exact running sum (a wrong
-// binade guess: the slice prefix was only estimated), is recomputed by the
-// whole workgroup with the iterative method, and the walk resumes after it.
+// Record gather of the finisher, issued right after its candidate loads so
+// that both travel in one round trip: every record's first kSpec words (its
+// head and one boundary lane) into the record area (s.Bk as words); records
+// with more boundary lanes take a second trip, one wave per record.
+// woff[slot] = LDS word offset, kSlotAbsent (no such segment) or
+// kSlotMissing (not in LDS, or not parked: summed again by the walk).
+constexpr uint32_t kSlotAbsent = 0xfffffffeu;
+constexpr uint32_t kSlotMissing = 0xffffffffu;
+
 template <int M>
-__device__ __forceinline__ void chain_slots(const KernelArgs& a, int b, uint32_t G, RowWs& ws,
-                                            uint32_t cap, Smem& s) {
+__device__ __forceinline__ void rec_gather(const KernelArgs& a, int b, uint32_t G, Smem& s) {
+  constexpr uint32_t kSpec = (4u + 3u + (uint32_t)M + 3u) & ~3u;  // nb <= 1, whole uint4s
   const uint32_t t = threadIdx.x, V = a.vocab;
-  const uint32_t chunk = (uint32_t)kThreads * M;
-  uint32_t* off = s.misc_slot;  // [0..kSlots]: record offsets; kSlots + j: slot id
-  if (t < 64u) {
-    uint32_t id = 0xffffffffu, size = 0;
-    uint32_t n = 0;
-    for (uint32_t i = 0; i < G; ++i) {
-      const Slice si = slice_bounds(V, G, i);
-      const uint32_t nq = (si.hi - si.lo + chunk - 1u) / chunk;
-      const uint32_t fi = __hip_atomic_load(&ws.part_fits[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      for (uint32_t q = 0; q < nq; ++q, ++n) {
-        if (n == t) {
-          id = i * kChainMaxQ + q;
-          if ((fi >> q) & 1u) size = ws.part_words[id];
-        }
-      }
+  uint32_t* woff = s.H + 1024;
+  uint32_t* longs = s.H + 1536;
+  uint32_t* words = reinterpret_cast<uint32_t*>(s.Bk);
+  constexpr uint32_t kCapWords = 2u * kCap;
+  uint4 rq[kSpec / 4];
+  uint32_t size = 0;
+  bool valid = false;
+  if (t < kRecSlots) {
+    const Slice r = rec_range<M>(V, G, t);
+    valid = t / ((uint32_t)kWaves * (uint32_t)kChainMaxQ) < G && r.lo < r.hi;
+    if (valid) {
+      const uint4* rec = reinterpret_cast<const uint4*>(rec_slot(a, b, t));
+#pragma unroll
+      for (int q = 0; q < (int)(kSpec / 4); ++q) rq[q] = rec[q];
     }
-    const uint32_t inc = wave_scan_incl(size, 0u, op_add_u32);
-    // records beyond the area count as missing (recomputed)
-    if (inc > cap) size = 0;
-    const uint32_t inc2 = wave_scan_incl(size, 0u, op_add_u32);
-    if (t < (uint32_t)kSlots) {
-      off[t] = inc2 - size;
-      off[kSlots + t] = id;
-      s.misc_size[t] = size;
+  }
+  LUMEN_TICK("g_heads_issued", b);
+  const bool parked = valid && rq[0].x != kRecNotParked;
+  if (parked) size = rec_words<M>(rq[0].x);
+  const uint32_t inc = block_incl_scan_u32(size, s);
+  LUMEN_TICK("g_heads_in", b);
+  const uint32_t off = inc - size;
+  const bool fits = parked && inc <= kCapWords;
+  if (t < kRecSlots) woff[t] = !valid ? kSlotAbsent : fits ? off : kSlotMissing;
+  if (t == 0) s.misc_u[2] = 0;
+  if (fits) {
+#pragma unroll
+    for (int q = 0; q < (int)(kSpec / 4); ++q) {
+      const uint32_t o = 4u * (uint32_t)q;
+      if (o < size) words[off + o] = rq[q].x;
+      if (o + 1u < size) words[off + o + 1u] = rq[q].y;
+      if (o + 2u < size) words[off + o + 2u] = rq[q].z;
+      if (o + 3u < size) words[off + o + 3u] = rq[q].w;
     }
-    if (t == 0) s.misc_u[3] = n;
-    if (t == 63u) s.misc_u[2] = inc2;
   }
   __syncthreads();
-}
-
-__device__ __forceinline__ void chain_gather_issue(const KernelArgs& a, int b, uint32_t* words,
-                                                   Smem& s) {
-  const uint32_t t = threadIdx.x;
-  const uint32_t* off = s.misc_slot;
-  const uint32_t nslots = s.misc_u[3];
-  const uint32_t total = s.misc_u[2];
-  for (uint32_t w = t; w < total; w += kThreads) {
-    uint32_t j = 0;
-    while (j + 1u < nslots && off[j + 1u] <= w) ++j;
-    const uint32_t id = off[kSlots + j];
-    words[w] = est_slot(a, b, id / kChainMaxQ, id % kChainMaxQ)[w - off[j]];
+  if (fits && size > kSpec) longs[atomicAdd(&s.misc_u[2], 1u)] = t | (off << 9);
+  __syncthreads();
+  const uint32_t nl = s.misc_u[2], lane = t & 63u;
+  LUMEN_TICK("g_heads_stored", b);
+  for (uint32_t k = t >> 6; k < nl; k += (uint32_t)kWaves) {
+    const uint32_t slot = longs[k] & 511u, o = longs[k] >> 9;
+    const uint32_t* rec = rec_slot(a, b, slot);
+    const uint32_t sz = rec_words<M>(words[o]);
+    for (uint32_t q0 = kSpec; q0 < sz; q0 += 256u) {
+      uint32_t tv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t q = q0 + 64u * (uint32_t)u + lane;
+        if (q < sz) tv[u] = rec[q];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t q = q0 + 64u * (uint32_t)u + lane;
+        if (q < sz) words[o + q] = tv[u];
+      }
+    }
   }
 }
 
+// Exact softmax sum of the row from the gathered records, on wave 0. A
+// record with a single run is a parity map in a known binade, so 64 such
+// records compose with one wave scan (the one-wave method of ecss.h with
+// records in place of elements); a record with boundary lanes, a run in
+// another binade, a crossing or a missing record stops the scan there and
+// is handled on its own. Returns the sum; *nre counts segments summed again.
 template <int M>
 __device__ __forceinline__ float chain_walk(const KernelArgs& a, int b, uint32_t G, const Row& row,
-                                            float m1, const uint32_t* words, Smem& s) {
+                                            float m1, uint32_t* nre_out, Smem& s) {
   const uint32_t t = threadIdx.x, V = a.vocab;
-  const uint32_t chunk = (uint32_t)kThreads * M;
-  const uint32_t* off = s.misc_slot;
-  const uint32_t nslots = s.misc_u[3];
-  float c = 0.f;
-  uint32_t j0 = 0;
-  while (j0 < nslots) {
-    if (t == 0) {
-      float cc = c;
-      uint32_t j = j0;
-      for (; j < nslots; ++j) {
-        if (s.misc_size[j] == 0u) break;
-        const uint32_t* r = words + off[j];
-        const uint32_t nb = r[0];
-        bool ok = true;
-        float y = cc;
-        for (uint32_t k = 0; k <= nb; ++k) {
-          const uint32_t sb = r[1u + 3u * k];
-          const uint32_t cb = __float_as_uint(y);
-          const uint32_t inc = (cb & 1u) ? r[3u + 3u * k] : r[2u + 3u * k];
-          const uint32_t nbits = cb + inc;
-          const bool run = sb != kEmptyRun;
-          if (run && ((cb & 0xff800000u) != sb || inc >= kSat || nbits >= sb + 0x00800000u)) {
-            ok = false;
-            break;
-          }
-          if (run) y = __uint_as_float(nbits);
-          if (k == nb) break;
-          const float* bx = reinterpret_cast<const float*>(r + 4u + 3u * nb) + k * (uint32_t)M;
-          float xq[M];
-#pragma unroll
-          for (int q = 0; q < M; ++q) xq[q] = bx[q];
-#pragma unroll
-          for (int q = 0; q < M; ++q) y = __fadd_rn(y, xq[q]);
+  const uint32_t nslots = G * (uint32_t)kChainMaxQ * (uint32_t)kWaves;
+  const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
+  const uint32_t* woff = s.H + 1024;
+  if (t < 64u) {
+    const uint32_t lane = t;
+    float c = 0.f;
+    uint32_t nre = 0;
+    for (uint32_t s0 = 0; s0 < nslots; s0 += 64u) {
+      const uint32_t sj = s0 + lane;
+      uint32_t wo = kSlotAbsent, nb = 0, sb = kEmptyRun, a0 = 0, a1 = 0;
+      if (sj < nslots) {
+        wo = woff[sj];
+        if (wo < kSlotAbsent) {
+          nb = words[wo];
+          sb = words[wo + 1];
+          a0 = words[wo + 2];
+          a1 = words[wo + 3];
         }
-        if (!ok) break;
-        cc = y;
       }
-      s.misc_u[0] = j;
-      s.red_f[0] = cc;
+      const bool present = wo != kSlotAbsent;
+      const bool simple = wo < kSlotAbsent && nb == 0u;
+      uint32_t t0 = 0;
+      for (;;) {
+        const uint32_t cb = __float_as_uint(c);
+        const uint32_t bin = cb & 0xff800000u;
+        const uint32_t ub = bin + 0x00800000u;
+        const bool act = lane >= t0 && present;
+        // an empty run (all-zero segment) is the identity in any binade
+        const bool fit = simple && (sb == bin || sb == kEmptyRun);
+        PMap m{0u, 0u};
+        if (act && fit && sb != kEmptyRun) m = PMap{a0, a1};
+        const PMap id{0u, 0u};
+        const PMap ex = wave_shr1(wave_scan_incl(m, id, pm_combine), id);
+        const uint32_t before = (cb & 1u) ? ex.a1 : ex.a0;
+        const uint32_t own = ((cb ^ before) & 1u) ? m.a1 : m.a0;
+        const uint32_t sbits = cb + before;
+        const uint32_t ebits = sbits + own;
+        const bool bad = act && (!fit || before >= kSat || own >= kSat || ebits >= ub);
+        const unsigned long long bm = __ballot(bad);
+        if (!bm) {
+          c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)ebits, 63));
+          break;
+        }
+        const int tb = __ffsll((long long)bm) - 1;
+        c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)sbits, tb));
+        const uint32_t wt = (uint32_t)__builtin_amdgcn_readlane((int)wo, tb);
+        const bool ok = wt < kSlotAbsent && rec_walk<M>(words + wt, c);
+        if (!ok) {
+#ifdef LUMEN_DEBUG_RECORDS
+          if (lane == 0 && b == 0)
+            printf("walk: slot %u %s at c=%a (nb %u)\n", s0 + (uint32_t)tb,
+                   wt >= kSlotAbsent ? "missing" : "mismatch", c,
+                   wt < kSlotAbsent ? words[wt] : 0u);
+#endif
+          c = seg_recompute<M>(row, rec_range<M>(V, G, s0 + (uint32_t)tb), m1, c);
+          ++nre;
+          LUMEN_TICK("walk_recomputed", b);
+        }
+        t0 = (uint32_t)tb + 1u;
+        if (t0 >= 64u) break;
+      }
     }
-    __syncthreads();
-    const uint32_t j = s.misc_u[0];
-    c = s.red_f[0];
-    __syncthreads();
-    if (j >= nslots) break;
-    // exact recomputation of slot j
-    const uint32_t id = off[kSlots + j];
-    const Slice si = slice_bounds(V, G, id / kChainMaxQ);
-    const uint32_t lo = si.lo + (id % kChainMaxQ) * chunk;
-    float x[M];
-    chain_load<M>(row, si, lo + t * (uint32_t)M, m1, x);
-    c = ecss_chunk<M>(c, x, kEcssSum, 0.f, s.ecss).c;
-    LUMEN_TICK("walk_recomputed", b);
-    j0 = j + 1u;
+    if (lane == 0) {
+      s.red_f[0] = c;
+      s.misc_i[0] = (int)nre;
+    }
   }
-  return c;
+  __syncthreads();
+  const float S1 = s.red_f[0];
+  *nre_out = (uint32_t)s.misc_i[0];
+  __syncthreads();
+  return S1;
 }
 
 // After the row barrier (m1 known): this workgroup's candidates, still in
@@ -1956,9 +2087,9 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
-  LUMEN_TICK("p_start", b + (int)sl);
+  LUMEN_TICK("p_start", b);
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
-  LUMEN_TICK("p_sampled", b + (int)sl);
+  LUMEN_TICK("p_sampled", b);
   const float tv = tau ? key2f(tau) : kNegInf;
   const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
   float mt = kNegInf;
@@ -1992,12 +2123,12 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     ws.part_nan[sl] = nan;
     ws.part_e[sl] = es_tot;
   }
-  LUMEN_TICK("p_pass1", b + (int)sl);
+  LUMEN_TICK("p_pass1", b);
   wg_arrive(&ws.bar, s);
   const bool ok = wg_wait_geq(&ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  LUMEN_TICK("p_barrier", b + (int)sl);
+  LUMEN_TICK("p_barrier", b);
   float m1 = kNegInf;
   uint32_t anynan = 0;
   double p_slice = 0.0;
@@ -2013,17 +2144,15 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   // path (uniform across the row once the barrier has completed)
   const bool single = anynan || !is_finite(m1) || ncand > (uint32_t)kCandCap;
   const bool m16 = sc_len_max(V, G) <= 16u * kThreads;
-  uint32_t fits = 0;
   if (ok && !single) {
     slice_candidates(a, b, sl, cand, my_base, my_n, m1, tau, s);
-    fits = m16 ? chain_prepare<16>(a, b, sl, row, sc, m1, p_slice, s)
-               : chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
+    if (m16) chain_prepare<16>(a, b, sl, row, sc, m1, p_slice, s);
+    else chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
   }
-  if (threadIdx.x == 0) ws.part_fits[sl] = fits;
-  LUMEN_TICK("p_prepared", b + (int)sl);
+  LUMEN_TICK("p_prepared", b);
   if (wg_arrive(&ws.arrive, s) != G - 1u) {
-    LUMEN_TICK("p_not_finisher", b + (int)sl);
-    LUMEN_TICK_DUMP(b + (int)sl);
+    LUMEN_TICK("p_not_finisher", b);
+    LUMEN_TICK_DUMP(b);
     return;
   }
   LUMEN_TICK("p_finisher", b);
@@ -2038,38 +2167,45 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   {
     const uint32_t t = threadIdx.x;
     const uint32_t nc = min(ncand, (uint32_t)kCap);
+    LUMEN_TICK("g_status_read", b);
     uint64_t c[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const uint32_t j = (uint32_t)q * kThreads + t;
       c[q] = j < nc ? cand[j] : 0ull;
     }
+    LUMEN_TICK("g_cands_issued", b);
     float hsum = 0.f;
     if (t < (uint32_t)kMassBins) {
       const float* hp = a.hist + (uint64_t)b * kMaxSlices * kMassBins + t;
-      for (uint32_t i = 0; i < G; ++i) hsum += hp[(uint64_t)i * kMassBins];
+      float hv[kMaxSlices];
+#pragma unroll
+      for (uint32_t i = 0; i < (uint32_t)kMaxSlices; ++i) hv[i] = i < G ? hp[(uint64_t)i * kMassBins] : 0.f;
+#pragma unroll
+      for (uint32_t i = 0; i < (uint32_t)kMaxSlices; ++i) hsum += hv[i];
     }
-    if (m16) chain_slots<16>(a, b, G, ws, 2u * kCap, s);
-    else chain_slots<32>(a, b, G, ws, 2u * kCap, s);
+    LUMEN_TICK("g_hist_in", b);
+    if (m16) rec_gather<16>(a, b, G, s);
+    else rec_gather<32>(a, b, G, s);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const uint32_t j = (uint32_t)q * kThreads + t;
       if (j < nc) s.A[j] = c[q];
     }
     if (t < (uint32_t)kMassBins) reinterpret_cast<float*>(s.H)[t] = hsum;
-    chain_gather_issue(a, b, reinterpret_cast<uint32_t*>(s.Bk), s);
     __syncthreads();
   }
   LUMEN_TICK("p_gathered", b);
-  const uint32_t* recs = reinterpret_cast<const uint32_t*>(s.Bk);
-  const float S1 = m16 ? chain_walk<16>(a, b, G, row, m1, recs, s)
-                       : chain_walk<32>(a, b, G, row, m1, recs, s);
+  uint32_t nre;
+  const float S1 = m16 ? chain_walk<16>(a, b, G, row, m1, &nre, s)
+                       : chain_walk<32>(a, b, G, row, m1, &nre, s);
   LUMEN_TICK("p_chain", b);
   RowTrace tr;
   init_trace(tr, V);
   tr.path = 4u;
   tr.passes = 2;
   tr.topp_sum = S1;
+  tr.pad[0] = nre;  // diagnostics: segments summed again by the walk
   topp_window(a, b, P, row, m1, S1, tau, ncand, rdraw, s, tr);
 }
 
@@ -2231,6 +2367,8 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
   uint32_t b, sl, G;
   block_row(a, b, sl, G);
   if (b >= a.batch) return;
+  LUMEN_TICK_SLOT(b, sl);
+  __syncthreads();
   if (G == 1u) {
     row_single(a, (int)b, s);
     return;
