@@ -672,35 +672,40 @@ __device__ __forceinline__ EcssResult row_ecss(const Row& r, X&& xf, int mode, f
   return e;
 }
 
-// ECSS over n elements of an LDS-resident list, x(j) for j < n.
-template <int M, class X>
-__device__ __forceinline__ EcssResult list_ecss_m(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
-  const uint32_t j0 = threadIdx.x * M;
-  float x[M];
-#pragma unroll
-  for (int q = 0; q < M; ++q) x[q] = (j0 + q < n) ? xf(j0 + q) : 0.f;
-  return ecss_fast_chunk<M>(c0, x, mode, theta, s.ecss, s.est, s.wsum, (int)min((uint32_t)kThreads, (n + (uint32_t)M - 1u) / (uint32_t)M));
-}
-
-// The one-wave method on a list of n <= 64 * M elements (wave 0 only).
-template <int M, class X>
+// The one-wave method on a list, in parts of 1024 elements (16 per lane);
+// the exact sum carries from part to part (wave 0 only).
+template <class X>
 __device__ __forceinline__ EcssResult list_ecss_wave(uint32_t n, X&& xf, int mode, float theta, float c0) {
-  const uint32_t j0 = (threadIdx.x & 63u) * M;
-  float x[M];
+  const uint32_t lane = threadIdx.x & 63u;
+  float c = c0;
+  for (uint32_t base = 0; base < n; base += 1024u) {
+    float x[16];
 #pragma unroll
-  for (int q = 0; q < M; ++q) x[q] = (j0 + q < n) ? xf(j0 + q) : 0.f;
-  return wave_ecss<M>(c0, x, mode, theta);
+    for (int q = 0; q < 16; ++q) {
+      const uint32_t j = base + lane * 16u + (uint32_t)q;
+      x[q] = j < n ? xf(j) : 0.f;
+    }
+    EcssResult r = wave_ecss<16>(c, x, mode, theta);
+    if (r.found) {
+      r.pos += (int)base;
+      return r;
+    }
+    c = r.c;
+  }
+  EcssResult r;
+  r.c = c;
+  r.found = 0;
+  r.pos = -1;
+  r.before = 0.f;
+  return r;
 }
 
 template <class X>
 __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, float theta, float c0, Smem& s) {
-  if (n <= 64u * 32u) {
-    // short lists: one wave, no workgroup barrier inside
+  {
+    // one wave, no workgroup barrier inside
     if (threadIdx.x < 64u) {
-      EcssResult r;
-      if (n <= 64u * 2u) r = list_ecss_wave<2>(n, xf, mode, theta, c0);
-      else if (n <= 64u * 8u) r = list_ecss_wave<8>(n, xf, mode, theta, c0);
-      else r = list_ecss_wave<32>(n, xf, mode, theta, c0);
+      const EcssResult r = list_ecss_wave(n, xf, mode, theta, c0);
       if (threadIdx.x == 0) {
         s.est.c_out = r.c;
         s.est.before = r.before;
@@ -717,10 +722,6 @@ __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, fl
     __syncthreads();
     return e;
   }
-  if (n <= 1024) return list_ecss_m<1>(n, xf, mode, theta, c0, s);
-  if (n <= 2048) return list_ecss_m<2>(n, xf, mode, theta, c0, s);
-  if (n <= 4096) return list_ecss_m<4>(n, xf, mode, theta, c0, s);
-  return list_ecss_m<8>(n, xf, mode, theta, c0, s);
 }
 
 // Walk over V tokens that all carry the same probability u (the uniform
@@ -1411,30 +1412,40 @@ __device__ __forceinline__ Slice slice_bounds(uint32_t V, uint32_t G, uint32_t s
 }
 
 // Makes this workgroup's global writes visible at device scope and arrives on
-// *ctr; returns the previous count (uniform across the workgroup).
-__device__ __forceinline__ uint32_t wg_arrive(uint32_t* ctr, Smem& s) {
+// *ctr; returns the previous count (uniform across the workgroup). The
+// arrival is a release only: an acquire at device scope invalidates the
+// whole L2 of this XCD (every workgroup there loses its cached lines), so it
+// is paid only by the workgroup that arrives last (old == last), which goes
+// on to read what the others wrote.
+__device__ __forceinline__ uint32_t wg_arrive(uint32_t* ctr, uint32_t last, Smem& s) {
   // every wave's stores have reached L2 once it passes the barrier; one
-  // device-scope release/acquire by thread 0 then covers the workgroup
+  // device-scope release by thread 0 then covers the workgroup
   __syncthreads();
-  if (threadIdx.x == 0)
-    s.misc_u[2] = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    s.misc_u[2] = old;
+  }
   __syncthreads();
   const uint32_t old = s.misc_u[2];
   __syncthreads();
   return old;
 }
 
-// Waits until *ctr >= target (acquire). Returns false on timeout.
+// Waits until *ctr >= target, then acquires. Returns false on timeout. The
+// counter is polled with relaxed loads (they read past this XCD's L2
+// without invalidating it); the one acquire comes after the wait.
 __device__ __forceinline__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem& s) {
   if (threadIdx.x == 0) {
     uint32_t n = 0, ok = 1;
-    while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
       __builtin_amdgcn_s_sleep(1);
       if (++n > kSpinLimit) {
         ok = 0;
         break;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     s.misc_u[3] = ok;
   }
   __syncthreads();
@@ -1551,7 +1562,7 @@ __device__ __forceinline__ void greedy_split(const KernelArgs& a, int b, uint32_
   }
   best = block_max_u64(best, s);
   if (threadIdx.x == 0) ws.part_arg[sl] = best;
-  const uint32_t old = wg_arrive(&ws.arrive, s);
+  const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
   if (old != G - 1u) return;
   uint64_t m = 0;
   for (uint32_t i = 0; i < G; ++i) {
@@ -1607,7 +1618,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   }
   flush_candidates(cand, &ws.cand_n, s);
   LUMEN_TICK("topk_compacted", b);
-  const uint32_t old = wg_arrive(&ws.arrive, s);
+  const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
   if (old != G - 1u) return;
   LUMEN_TICK("topk_finisher", b);
   const uint32_t n = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2124,7 +2135,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     ws.part_e[sl] = es_tot;
   }
   LUMEN_TICK("p_pass1", b);
-  wg_arrive(&ws.bar, s);
+  wg_arrive(&ws.bar, 0xffffffffu, s);
   const bool ok = wg_wait_geq(&ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2150,7 +2161,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     else chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
   }
   LUMEN_TICK("p_prepared", b);
-  if (wg_arrive(&ws.arrive, s) != G - 1u) {
+  if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) {
     LUMEN_TICK("p_not_finisher", b);
     LUMEN_TICK_DUMP(b);
     return;
@@ -2340,15 +2351,15 @@ __device__ __forceinline__ void row_exit(const KernelArgs& a, Smem& s) {
   uint32_t b, sl, G;
   block_row(a, b, sl, G);
   RowWs& ws = a.ws[b];
-  const uint32_t old = wg_arrive(&ws.exit_, s);
+  // nothing written by the others is read here, so no acquire; the next
+  // launch sees the cleared block (kernel boundary)
+  const uint32_t old = wg_arrive(&ws.exit_, 0xffffffffu, s);
   if (old == G - 1u && threadIdx.x == 0) {
     ws.arrive = 0;
     ws.bar = 0;
     ws.cand_n = 0;
     ws.status = 0;
-    __threadfence();
     ws.exit_ = 0;
-    __threadfence();
   }
 }
 
