@@ -111,6 +111,8 @@ struct KernelArgs {
   const uint32_t* blk_map;
   uint32_t inline_rows;      // > 0: params come from inline_params
   uint32_t inline_draws;     // != 0: draws come from inline_uniforms
+  uint32_t debug_stop;       // development aid: split top-p rows stop after phase k (0: off)
+  uint32_t pad1;
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };

@@ -433,6 +433,14 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
                                                   (uint32_t)s->max_resident / padded));
   ka.slices = G;
   ka.xcd_rows = (B >= 8 && G > 1) ? 1u : 0u;
+  {
+    // development aid (phase costs on the critical path): LUMEN_SAMPLER_DEBUG_STOP=k
+    static const uint32_t stop = [] {
+      const char* e = std::getenv("LUMEN_SAMPLER_DEBUG_STOP");
+      return e ? (uint32_t)std::strtoul(e, nullptr, 10) : 0u;
+    }();
+    ka.debug_stop = stop;
+  }
   uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
   if (G > 1 && B >= 8 && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
     nblocks = plan_blocks(rows, V, (uint32_t)s->max_resident, s->blk_map);

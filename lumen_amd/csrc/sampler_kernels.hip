@@ -886,12 +886,167 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
   return V - 1;
 }
 
+// One-wave small path: everything after top-k for a list of at most
+// kWaveList entries (s.A, (idx << 32) | key, ascending idx) whose maximum is
+// finite and that holds no NaN. Lane l holds entries 4l .. 4l + 3, so the
+// lane-major order is index order. The list top-p sorts by (p desc, idx
+// asc) through ranks (each lane counts the keys below its own, read as LDS
+// broadcasts), and every sequential sum is the one-wave exact method.
+// Returns false (uniform), having written nothing, when the list needs the
+// general path (uniform branches, NaN, or a non-finite temperature product).
+constexpr uint32_t kWaveList = 256;
+
+__device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, const RowParams& P,
+                                                uint32_t n, bool topp_done, float r, Smem& s,
+                                                RowTrace& tr) {
+  const uint32_t t = threadIdx.x, V = a.vocab;
+  uint64_t* keys = s.Bk;          // [kWaveList] sort keys, then by rank
+  float* sp = reinterpret_cast<float*>(s.Bk + kWaveList);  // [kWaveList] p by rank
+  if (t < 64u) {
+    const uint32_t lane = t;
+    uint32_t idx[4];
+    float v[4];
+    bool val[4];
+    float m = kNegInf;
+    bool nan = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t j = 4u * lane + (uint32_t)q;
+      val[q] = j < n;
+      const uint64_t e = val[q] ? s.A[j] : 0ull;
+      idx[q] = (uint32_t)(e >> 32);
+      v[q] = val[q] ? key2f((uint32_t)e) : kNegInf;
+      nan |= val[q] && is_nan(v[q]);
+      m = rmax(m, v[q]);
+    }
+    m = wave_reduce(m, kNegInf, rmax);
+    nan = __ballot(nan) != 0ull;
+    bool ok = is_finite(m) && !nan;
+    bool kept[4] = {val[0], val[1], val[2], val[3]};
+    float tp_sum = 0.f, tp_cum = 0.f;
+    uint32_t tp_kept = 0;
+    const bool do_topp = ok && (P.flags & kTopP) && !topp_done;
+    if (do_topp) {
+      // top-p on the list (sampling.rs:942-967): softmax at T = 1 in index
+      // order, then the cumulative sum in (p desc, idx asc) order
+      float ex[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ex[q] = val[q] ? expf_glibc(__fsub_rn(v[q], m)) : 0.f;
+      const float S1 = wave_ecss<4>(0.f, ex, kEcssSum, 0.f).c;
+      uint64_t key[4];
+      float p[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        p[q] = val[q] ? __fdiv_rn(ex[q], S1) : 0.f;
+        key[q] = val[q] ? (((uint64_t)(~__float_as_uint(p[q])) << 32) | idx[q]) : ~0ull;
+        if (val[q]) keys[4u * lane + (uint32_t)q] = key[q];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // keys past n read as all-ones (never below a live key)
+      for (uint32_t j = n + lane; j < ((n + 15u) & ~15u); j += 64u) keys[j] = ~0ull;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      uint32_t rk[4] = {0u, 0u, 0u, 0u};
+      for (uint32_t i0 = 0; i0 < n; i0 += 16u) {
+        uint64_t kb[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) kb[u] = keys[i0 + (uint32_t)u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) rk[q] += kb[u] < key[q] ? 1u : 0u;
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (val[q]) sp[rk[q]] = p[q];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float ps[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ps[q] = val[q] ? sp[4u * lane + (uint32_t)q] : 0.f;
+      const EcssResult w = wave_ecss<4>(0.f, ps, kEcssFindGe, P.top_p);
+      tp_sum = S1;
+      tp_cum = w.c;
+      tp_kept = w.found ? (uint32_t)w.pos + 1u : V;
+      if (w.found) {
+        // the entry at sorted position w.pos: the one whose rank equals it
+        uint64_t kst = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) kst = (val[q] && rk[q] == (uint32_t)w.pos) ? key[q] : kst;
+        kst = wave_reduce(kst, (uint64_t)0, op_max_u64);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) kept[q] = val[q] && key[q] <= kst;
+      }
+    }
+    // min-p (sampling.rs:976-994): the bound comes from the surviving
+    // maximum, which top-p always keeps (it has the largest p)
+    if (ok && (P.flags & kMinP)) {
+      const float bound = __fadd_rn(m, P.log_min_p);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) kept[q] = kept[q] && !(v[q] < bound);
+    }
+    // temperature, softmax, inverse-CDF draw (sampling.rs:516-526, 1003-1014)
+    float wv[4];
+    float m3 = kNegInf;
+    bool nan3 = false;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wv[q] = kept[q] ? __fmul_rn(v[q], P.inv_temp) : kNegInf;
+      nan3 |= kept[q] && is_nan(wv[q]);
+      m3 = rmax(m3, wv[q]);
+    }
+    m3 = wave_reduce(m3, kNegInf, rmax);
+    ok = ok && is_finite(m3) && __ballot(nan3) == 0ull;
+    if (ok) {
+      float e3[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e3[q] = kept[q] ? expf_glibc(__fsub_rn(wv[q], m3)) : 0.f;
+      const float S3 = wave_ecss<4>(0.f, e3, kEcssSum, 0.f).c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) e3[q] = kept[q] ? __fdiv_rn(e3[q], S3) : 0.f;
+      const EcssResult e = wave_ecss<4>(0.f, e3, kEcssFindGt, r);
+      uint32_t tok = V - 1u;
+      if (e.found) {
+        const int qq = e.pos & 3;
+        const uint32_t ix = qq == 0 ? idx[0] : qq == 1 ? idx[1] : qq == 2 ? idx[2] : idx[3];
+        tok = (uint32_t)__builtin_amdgcn_readlane((int)ix, e.pos >> 2);
+      }
+      if (lane == 0) {
+        tr.path |= 2u;
+        if (do_topp) {
+          tr.topp_sum = tp_sum;
+          tr.topp_kept = tp_kept;
+          tr.topp_cum = tp_cum;
+        }
+        tr.final_max = m3;
+        tr.final_sum = S3;
+        tr.cdf_before = e.found ? e.before : e.c;
+        tr.cdf_at = e.c;
+        s.misc_u[0] = tok;
+      }
+    }
+    if (lane == 0) s.misc_u[1] = ok ? 1u : 0u;
+  }
+  __syncthreads();
+  const bool handled = s.misc_u[1] != 0u;
+  const uint32_t tok = s.misc_u[0];
+  __syncthreads();
+  if (handled) write_result(a, b, tok, tr);
+  return handled;
+}
+
 // Everything after top-k for a row whose survivors are in s.A as
 // (idx << 32) | key, ascending idx (sampling.rs:502-526): top-p on the list
 // (unless already applied), min-p, temperature, softmax, draw.
 __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const RowParams& P, uint32_t nlist,
                            bool topp_done, float rdraw, Smem& s, RowTrace& tr,
                            float known_max = __builtin_nanf("")) {
+  if (nlist <= kWaveList && wave_small_path(a, b, P, nlist, topp_done, rdraw, s, tr)) return;
   const int t = threadIdx.x;
   const uint32_t V = a.vocab;
   tr.path |= 2u;
@@ -984,6 +1139,10 @@ __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const Row
     nlist = nk;
   }
   LUMEN_TICK("small_before_final", b);
+  if ((a.debug_stop >> 8) == 6u && !(P.flags & kTopP && tr.path == 4u)) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr, known_max);
   LUMEN_TICK("small_after_final", b);
   write_result(a, b, tok, tr);
@@ -1592,6 +1751,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   LUMEN_TICK("topk_start", b);
   const uint32_t tau = sample_threshold(row, V, target, s);
   LUMEN_TICK("topk_sampled", b);
+  if ((a.debug_stop >> 8) == 1u) return;
   const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
   if (threadIdx.x == 0) s.cnt = 0;
   __syncthreads();
@@ -1618,6 +1778,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   }
   flush_candidates(cand, &ws.cand_n, s);
   LUMEN_TICK("topk_compacted", b);
+  if ((a.debug_stop >> 8) == 2u) return;
   const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
   if (old != G - 1u) return;
   LUMEN_TICK("topk_finisher", b);
@@ -1632,6 +1793,10 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) s.A[j] = cand[j];
   __syncthreads();
   LUMEN_TICK("topk_loaded", b);
+  if ((a.debug_stop >> 8) == 3u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   // candidate entries are (~key << 32) | idx
   auto ckey = [&](uint32_t j) { return ~(uint32_t)(s.A[j] >> 32); };
   uint32_t cut, ns;
@@ -1668,12 +1833,20 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     ns = s.cnt;
   }
   LUMEN_TICK("topk_sort1", b);
+  if ((a.debug_stop >> 8) == 4u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   for (uint32_t j = threadIdx.x; j < ns; j += kThreads) s.A[j] = s.Bk[j];
   __syncthreads();
   sort_u64_asc(s.A, ns, s.Bk, s);  // ascending index
   tr.topk_cutoff_key = cut;
   tr.topk_survivors = ns;
   LUMEN_TICK("topk_sorted", b);
+  if ((a.debug_stop >> 8) == 5u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   small_path(a, b, P, ns, false, rdraw, s, tr);
   LUMEN_TICK("topk_done", b);
 }
@@ -2101,6 +2274,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   LUMEN_TICK("p_start", b);
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
   LUMEN_TICK("p_sampled", b);
+  if ((a.debug_stop & 255u) == 1u) return;
   const float tv = tau ? key2f(tau) : kNegInf;
   const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
   float mt = kNegInf;
@@ -2135,11 +2309,13 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     ws.part_e[sl] = es_tot;
   }
   LUMEN_TICK("p_pass1", b);
+  if ((a.debug_stop & 255u) == 2u) return;
   wg_arrive(&ws.bar, 0xffffffffu, s);
   const bool ok = wg_wait_geq(&ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("p_barrier", b);
+  if ((a.debug_stop & 255u) == 3u) return;
   float m1 = kNegInf;
   uint32_t anynan = 0;
   double p_slice = 0.0;
@@ -2161,6 +2337,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     else chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
   }
   LUMEN_TICK("p_prepared", b);
+  if ((a.debug_stop & 255u) == 4u) return;
   if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) {
     LUMEN_TICK("p_not_finisher", b);
     LUMEN_TICK_DUMP(b);
@@ -2207,10 +2384,18 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     __syncthreads();
   }
   LUMEN_TICK("p_gathered", b);
+  if ((a.debug_stop & 255u) == 5u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   uint32_t nre;
   const float S1 = m16 ? chain_walk<16>(a, b, G, row, m1, &nre, s)
                        : chain_walk<32>(a, b, G, row, m1, &nre, s);
   LUMEN_TICK("p_chain", b);
+  if ((a.debug_stop & 255u) == 6u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   RowTrace tr;
   init_trace(tr, V);
   tr.path = 4u;
@@ -2284,6 +2469,10 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   const uint32_t n = s.cnt;
   LUMEN_TICK("p_window_built", b);
+  if ((a.debug_stop & 255u) == 7u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   {
     // keys (~p bits << 32) | id with p in [p_lo, 1/S1]: their common high
     // bits are known without a reduction
@@ -2292,10 +2481,18 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
     sort_u64_asc(s.Bk, n, s.A, s, hint);
   }
   LUMEN_TICK("p_window_sorted", b);
+  if ((a.debug_stop & 255u) == 8u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   EcssResult wk = list_ecss(
       n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe,
       P.top_p, 0.f, s);
   LUMEN_TICK(s.est.fail == 2 ? "p_walk_nofit" : s.est.fail ? "p_walk_failed" : "p_walk_ok", b);
+  if ((a.debug_stop & 255u) == 9u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   if (!wk.found) {
     row_single(a, b, s);
     return;
@@ -2311,6 +2508,10 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   sort_u64_asc(s.A, nk, s.Bk, s, ((uint64_t)span_mask(a.vocab) << 32) | 0xffffffffull);
   LUMEN_TICK("p_kept_sorted", b);
+  if ((a.debug_stop & 255u) == 10u) {
+    if (threadIdx.x == 0) a.tokens[b] = 0u;
+    return;
+  }
   // the kept set holds the row maximum m1
   small_path(a, b, P, nk, true, rdraw, s, tr, m1);
 }
