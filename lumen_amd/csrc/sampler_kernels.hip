@@ -672,6 +672,11 @@ __device__ __forceinline__ EcssResult row_ecss(const Row& r, X&& xf, int mode, f
   return e;
 }
 
+// Position of element j in a padded float array: one spare word after every
+// 16, so the lanes of a wave reading 16 consecutive elements each (17 words
+// apart) hit different LDS banks.
+__device__ __forceinline__ uint32_t pad16(uint32_t j) { return j + (j >> 4); }
+
 // The one-wave method on a list, in parts of 1024 elements (16 per lane);
 // the exact sum carries from part to part (wave 0 only).
 template <class X>
@@ -869,15 +874,15 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
   // the summands, then the probabilities, computed by the whole workgroup
   // into LDS (list B is free here); the exact sums read them back
   float* xs = reinterpret_cast<float*>(s.Bk);
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = expf_glibc(__fsub_rn(wv(j), m3));
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[pad16(j)] = expf_glibc(__fsub_rn(wv(j), m3));
   __syncthreads();
-  EcssResult S = list_ecss(n, [&](uint32_t j) { return xs[j]; }, kEcssSum, 0.f, 0.f, s);
+  EcssResult S = list_ecss(n, [&](uint32_t j) { return xs[pad16(j)]; }, kEcssSum, 0.f, 0.f, s);
   const float S3 = S.c;
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[pad16(j)] = __fdiv_rn(xs[pad16(j)], S3);
   __syncthreads();
   LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", 0);
   tr.final_sum = S3;
-  EcssResult e = list_ecss(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
+  EcssResult e = list_ecss(n, [&](uint32_t j) { return xs[pad16(j)]; }, kEcssFindGt, r, 0.f, s);
   LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", 0);
   LUMEN_TICK("fin_walk", 0);
   tr.cdf_before = e.found ? e.before : e.c;
@@ -2492,9 +2497,13 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
-  EcssResult wk = list_ecss(
-      n, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe,
-      P.top_p, 0.f, s);
+  // the sorted probabilities into a padded float array (list A is free
+  // after the sort)
+  float* ps = reinterpret_cast<float*>(s.A);
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads)
+    ps[pad16(j)] = __uint_as_float(~(uint32_t)(s.Bk[j] >> 32));
+  __syncthreads();
+  EcssResult wk = list_ecss(n, [&](uint32_t j) { return ps[pad16(j)]; }, kEcssFindGe, P.top_p, 0.f, s);
   LUMEN_TICK(s.est.fail == 2 ? "p_walk_nofit" : s.est.fail ? "p_walk_failed" : "p_walk_ok", b);
   if ((a.debug_stop & 255u) == 9u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
