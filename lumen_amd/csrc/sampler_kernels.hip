@@ -901,13 +901,45 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
 // general path (uniform branches, NaN, or a non-finite temperature product).
 constexpr uint32_t kWaveList = 256;
 
+// The reference's own sequential f32 loop over xs[0..n) (LDS), run by every
+// lane of the wave on broadcast reads, 16 loads ahead of the dependent adds.
+// For short lists this is cheaper than the parity-map method, whose cost
+// grows with the number of binades the sum crosses.
+__device__ __forceinline__ EcssResult seq_ecss(const float* xs, uint32_t n, int mode, float theta) {
+  float c = 0.f, prev = 0.f;
+  int pos = -1;
+  for (uint32_t j0 = 0; j0 < n && pos < 0; j0 += 16u) {
+    float xv[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) xv[q] = (j0 + (uint32_t)q < n) ? xs[j0 + q] : 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (pos < 0) {
+        const float y = __fadd_rn(c, xv[q]);
+        if (mode != kEcssSum && j0 + (uint32_t)q < n && ecss_cond(mode, y, theta)) {
+          pos = (int)(j0 + (uint32_t)q);
+          prev = c;
+        }
+        c = y;
+      }
+    }
+  }
+  EcssResult r;
+  r.c = c;
+  r.before = prev;
+  r.found = pos >= 0 ? 1 : 0;
+  r.pos = pos;
+  return r;
+}
+
 __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, const RowParams& P,
                                                 uint32_t n, bool topp_done, float r, Smem& s,
                                                 RowTrace& tr) {
   const uint32_t t = threadIdx.x, V = a.vocab;
   uint64_t* keys = s.Bk;          // [kWaveList] sort keys, then by rank
   float* sp = reinterpret_cast<float*>(s.Bk + kWaveList);  // [kWaveList] p by rank
-  if (t < 64u) {
+  float* xs = sp + kWaveList;     // [kWaveList] summands in index order
+  if (t < 64u) do {
     const uint32_t lane = t;
     uint32_t idx[4];
     float v[4];
@@ -936,8 +968,14 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
       // order, then the cumulative sum in (p desc, idx asc) order
       float ex[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ex[q] = val[q] ? expf_glibc(__fsub_rn(v[q], m)) : 0.f;
-      const float S1 = wave_ecss<4>(0.f, ex, kEcssSum, 0.f).c;
+      for (int q = 0; q < 4; ++q) {
+        ex[q] = val[q] ? expf_glibc(__fsub_rn(v[q], m)) : 0.f;
+        if (val[q]) xs[4u * lane + (uint32_t)q] = ex[q];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float S1 = seq_ecss(xs, n, kEcssSum, 0.f).c;
       uint64_t key[4];
       float p[4];
 #pragma unroll
@@ -971,10 +1009,7 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      float ps[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) ps[q] = val[q] ? sp[4u * lane + (uint32_t)q] : 0.f;
-      const EcssResult w = wave_ecss<4>(0.f, ps, kEcssFindGe, P.top_p);
+      const EcssResult w = seq_ecss(sp, n, kEcssFindGe, P.top_p);
       tp_sum = S1;
       tp_cum = w.c;
       tp_kept = w.found ? (uint32_t)w.pos + 1u : V;
@@ -1010,11 +1045,22 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
     if (ok) {
       float e3[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) e3[q] = kept[q] ? expf_glibc(__fsub_rn(wv[q], m3)) : 0.f;
-      const float S3 = wave_ecss<4>(0.f, e3, kEcssSum, 0.f).c;
+      for (int q = 0; q < 4; ++q) {
+        e3[q] = kept[q] ? expf_glibc(__fsub_rn(wv[q], m3)) : 0.f;
+        if (val[q]) xs[4u * lane + (uint32_t)q] = e3[q];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float S3 = seq_ecss(xs, n, kEcssSum, 0.f).c;
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int q = 0; q < 4; ++q) e3[q] = kept[q] ? __fdiv_rn(e3[q], S3) : 0.f;
-      const EcssResult e = wave_ecss<4>(0.f, e3, kEcssFindGt, r);
+      for (int q = 0; q < 4; ++q)
+        if (val[q]) xs[4u * lane + (uint32_t)q] = kept[q] ? __fdiv_rn(e3[q], S3) : 0.f;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const EcssResult e = seq_ecss(xs, n, kEcssFindGt, r);
       uint32_t tok = V - 1u;
       if (e.found) {
         const int qq = e.pos & 3;
@@ -1036,7 +1082,7 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
       }
     }
     if (lane == 0) s.misc_u[1] = ok ? 1u : 0u;
-  }
+  } while (0);
   __syncthreads();
   const bool handled = s.misc_u[1] != 0u;
   const uint32_t tok = s.misc_u[0];
