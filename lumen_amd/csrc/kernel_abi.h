@@ -70,7 +70,7 @@ constexpr int kRecWords = 1152;     // words per run record slot
 struct RowWs {
   uint32_t arrive;       // last-arriver counter
   uint32_t bar;          // spin barrier counter
-  uint32_t exit_;        // exit counter (resets the block)
+  uint32_t unused0;
   uint32_t cand_n;       // candidates appended
   uint32_t status;       // row failure bits
   uint32_t pad[3];

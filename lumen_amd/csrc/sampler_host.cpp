@@ -55,7 +55,7 @@ RowPath row_path(const RowParams& r, uint32_t V, uint32_t G) {
 // co-resident. Returns the grid size; map[block] = (row << 10) | (G << 5) |
 // slice, or kIdleBlock.
 uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t cap,
-                     std::vector<uint32_t>& map) {
+                     uint32_t g_uniform, std::vector<uint32_t>& map) {
   const uint32_t B = (uint32_t)rows.size();
   const uint32_t kX = 8;
   const uint32_t bin_cap = cap / kX;
@@ -80,6 +80,14 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
     uint64_t g = wsum ? ((uint64_t)spare * w[b] + wsum / 2) / wsum : 1;
     G[b] = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(g, lumen::kMaxSlices));
     if (row_path(rows[b], V, G[b]) == kPathTopP && G[b] < gmin_topp) G[b] = 1;
+  }
+  // every row at g_uniform: the kernel's arithmetic mapping places the same
+  // grid without a map (one dependent load less per workgroup)
+  bool uniform = true;
+  for (uint32_t b = 0; b < B; ++b) uniform = uniform && w[b] && G[b] == g_uniform;
+  if (uniform) {
+    map.clear();
+    return 0;
   }
   // pack rows (largest first) into the XCD lists
   std::vector<uint32_t> order(B);
@@ -443,8 +451,11 @@ int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_st
   }
   uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
   if (G > 1 && B >= 8 && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
-    nblocks = plan_blocks(rows, V, (uint32_t)s->max_resident, s->blk_map);
-    ka.slices = lumen::kMaxSlices;  // buffers are sized for the largest G
+    const uint32_t nb = plan_blocks(rows, V, (uint32_t)s->max_resident, G, s->blk_map);
+    if (nb) {
+      nblocks = nb;
+      ka.slices = lumen::kMaxSlices;  // buffers are sized for the largest G
+    }
   } else {
     s->blk_map.clear();
   }

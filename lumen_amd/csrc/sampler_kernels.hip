@@ -99,6 +99,7 @@ struct Smem {
   uint32_t red_b[kWaves];
   float red_f[kWaves];
   uint32_t cnt;
+  uint32_t finisher;  // this workgroup arrived last on its row's counter
   int misc_i[4];
   uint32_t misc_u[4];
 };
@@ -1633,7 +1634,10 @@ __device__ __forceinline__ uint32_t wg_arrive(uint32_t* ctr, uint32_t last, Smem
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (old == last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      s.finisher = 1u;
+    }
     s.misc_u[2] = old;
   }
   __syncthreads();
@@ -2607,22 +2611,18 @@ __device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint
   }
 }
 
-// The last workgroup of a row to leave restores its coordination block. The
-// row is derived again from the block index, so nothing has to stay live
-// across the path calls.
-__device__ __forceinline__ void row_exit(const KernelArgs& a, Smem& s) {
-  uint32_t b, sl, G;
-  block_row(a, b, sl, G);
-  RowWs& ws = a.ws[b];
-  // nothing written by the others is read here, so no acquire; the next
-  // launch sees the cleared block (kernel boundary)
-  const uint32_t old = wg_arrive(&ws.exit_, 0xffffffffu, s);
-  if (old == G - 1u && threadIdx.x == 0) {
+// The workgroup that arrived last on its row's counter restores the row's
+// coordination block once it is done. Every other workgroup of the row has
+// arrived before it and no longer touches the block; the next launch sees
+// the cleared block (kernel boundary).
+__device__ __forceinline__ void row_reset(const KernelArgs& a, uint32_t b, Smem& s) {
+  __syncthreads();
+  if (threadIdx.x == 0 && s.finisher) {
+    RowWs& ws = a.ws[b];
     ws.arrive = 0;
     ws.bar = 0;
     ws.cand_n = 0;
     ws.status = 0;
-    ws.exit_ = 0;
   }
 }
 
@@ -2636,6 +2636,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
       *reinterpret_cast<const KernelArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
   __shared__ Smem s;
   LUMEN_TICK_INIT();
+  if (threadIdx.x == 0) s.finisher = 0u;
   expf_table_init();
   __syncthreads();
   uint32_t b, sl, G;
@@ -2663,6 +2664,6 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
       row_single(a, (int)b, s);
     }
   }
-  row_exit(a, s);
+  row_reset(a, b, s);
 }
 }  // namespace lumen
