@@ -113,6 +113,12 @@ struct KernelArgs {
   uint32_t inline_draws;     // != 0: draws come from inline_uniforms
   uint32_t debug_stop;       // development aid: split top-p rows stop after phase k (0: off)
   uint32_t pad1;
+  // Synchronous calls: the token is also written to pinned host memory
+  // mapped into the device, and *done_mapped (host memory) counts the rows
+  // written, so the host waits on that count instead of a copy and a stream
+  // synchronization. NULL otherwise.
+  uint32_t* tokens_mapped;
+  uint32_t* done_mapped;
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };

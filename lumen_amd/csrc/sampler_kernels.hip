@@ -801,6 +801,10 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
       tr.token = token;
       a.trace[b] = tr;
     }
+    if (a.tokens_mapped) {
+      a.tokens_mapped[b] = token;
+      __hip_atomic_fetch_add(a.done_mapped, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 }
 
