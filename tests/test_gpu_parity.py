@@ -294,3 +294,30 @@ def test_config5_full(eng):
     from lumen_amd.workloads import config5
 
     _run_workload(eng, config5(), n_rows=32)
+
+
+def test_config4_full(eng):
+    # B=256 bf16 rows over a flat distribution with top_p 0.99: the nucleus
+    # spans most of the vocabulary (the sort / prefix-sum worst case)
+    from lumen_amd.workloads import config4
+
+    _run_workload(eng, config4())
+
+
+def test_config2_sequential_draws(eng):
+    # B=1 latency workload: successive draws from one Xorshift64 stream, each
+    # sampled token recorded into the history (Sampler::sample,
+    # sampling.rs:429-433), so the penalties change from draw to draw
+    from lumen_amd.sampling import Xorshift64
+    from lumen_amd.workloads import config2
+
+    w = config2()
+    rng = Xorshift64(w.seeds[0])
+    hist = np.asarray(w.histories[0], dtype=np.uint32)
+    lg = w.logits_f32()
+    for d in range(12):
+        u = np.array([rng.next_f32()], np.float32)
+        log(f"case config2 draw {d} history {hist.size}")
+        rep = parity.compare(eng, lg, w.params, [hist], u, check_pen=True)
+        assert_clean(rep, f"config2 draw {d}")
+        hist = np.append(hist, np.uint32(rep["gpu"][0]))
