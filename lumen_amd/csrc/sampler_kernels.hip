@@ -1815,6 +1815,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
   LUMEN_TICK("topk_start", b);
+  if ((a.debug_stop >> 8) == 15u) return;
   const uint32_t tau = sample_threshold(row, V, target, s);
   LUMEN_TICK("topk_sampled", b);
   if ((a.debug_stop >> 8) == 1u) return;
@@ -2338,6 +2339,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
   LUMEN_TICK("p_start", b);
+  if ((a.debug_stop & 255u) == 15u) return;
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
   LUMEN_TICK("p_sampled", b);
   if ((a.debug_stop & 255u) == 1u) return;
