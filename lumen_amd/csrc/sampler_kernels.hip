@@ -307,10 +307,13 @@ __device__ __forceinline__ void clear_hist(uint32_t* H, int nb) {
 
 // Key of 0-based rank r in descending order among key(j), j < n (n > r):
 // three LDS histogram rounds over 11/11/10-bit digits.
+// With levels < 3 the result is the lower edge of the bucket holding the
+// r-th largest key: a lower bound with at least r + 1 keys at or above it.
 template <class K>
-__device__ __forceinline__ uint32_t select_desc(uint32_t n, K&& key, uint32_t r, Smem& s) {
+__device__ __forceinline__ uint32_t select_desc(uint32_t n, K&& key, uint32_t r, Smem& s,
+                                                int levels = 3) {
   uint32_t prefix = 0, pmask = 0, need = r + 1u;
-  for (int lvl = 0; lvl < 3; ++lvl) {
+  for (int lvl = 0; lvl < levels; ++lvl) {
     const int sh = lvl == 0 ? 21 : (lvl == 1 ? 10 : 0);
     const int nb = lvl == 2 ? 1024 : 2048;
     const uint32_t dm = (uint32_t)nb - 1u;
@@ -1801,6 +1804,52 @@ __device__ __forceinline__ void greedy_split(const KernelArgs& a, int b, uint32_
   write_result(a, b, 0xffffffffu - (uint32_t)m, tr);
 }
 
+// Candidates of a short top-k slice (at most 16 elements per thread) without
+// sampling: with the slice in registers, every thread's largest
+// non-history key is found, and two radix levels over those kThreads keys
+// give a lower bound tau of their k-th largest (k <= kThreads). At least k
+// elements of the slice have keys >= tau, so tau is at most the slice's
+// k-th largest key, which is at most the row's: every key of the row's top
+// k is >= tau. Non-history elements with keys >= tau are appended to list A
+// (history ids are handled by the caller with their penalized values). Key
+// 0 stands for "not a candidate".
+__device__ __forceinline__ uint32_t topk_collect16(const Row& row, Slice sc, const uint32_t* bm,
+                                                   uint32_t k, Smem& s) {
+  const uint32_t t = threadIdx.x;
+  uint32_t kk[4][4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t i = sc.lo + ((uint32_t)q * kThreads + t) * 4u;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (i < sc.hi) row.load4(i, v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kk[q][j] = i + (uint32_t)j < sc.hi ? tkey(v[j]) : 0u;
+  }
+  uint32_t tm = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = sc.lo + ((uint32_t)q * kThreads + t) * 4u + (uint32_t)j;
+      if (bm && kk[q][j] != 0u && bm_test(bm, i - sc.lo)) kk[q][j] = 0u;
+      tm = max(tm, kk[q][j]);
+    }
+  uint32_t* tk = reinterpret_cast<uint32_t*>(s.A);
+  tk[t] = tm;
+  __syncthreads();
+  const uint32_t tau = select_desc((uint32_t)kThreads, [&](uint32_t j) { return tk[j]; }, k - 1u, s, 2);
+  if (t == 0) s.cnt = 0;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = sc.lo + ((uint32_t)q * kThreads + t) * 4u + (uint32_t)j;
+      list_push(s.A, &s.cnt, kk[q][j] != 0u && kk[q][j] >= tau, ((uint64_t)(~kk[q][j]) << 32) | i);
+    }
+  return tau;
+}
+
 // Top-k: a sampled threshold, one compaction pass per slice into the row's
 // candidate buffer, and the last workgroup finishes on the LDS list. If the
 // sample missed (fewer than k or more than the buffer holds), the finisher
@@ -1813,20 +1862,30 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   const Slice sc = slice_bounds(V, G, sl);
   const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
-  const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
   LUMEN_TICK("topk_start", b);
   if ((a.debug_stop >> 8) == 15u) return;
-  const uint32_t tau = sample_threshold(row, V, target, s);
-  LUMEN_TICK("topk_sampled", b);
-  if ((a.debug_stop >> 8) == 1u) return;
-  const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
-  if (threadIdx.x == 0) s.cnt = 0;
-  __syncthreads();
-  range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
-    const uint32_t kk = tkey(v);
-    const bool in = kk >= tau && !(pen && bm_test(bm, i - sc.lo));
-    list_push(s.A, &s.cnt, in, ((uint64_t)(~kk) << 32) | i);
-  });
+  uint32_t tau;
+  const uint32_t* bm;
+  if (k <= (uint32_t)kThreads && sc_len_max(V, G) <= 16u * kThreads) {
+    // short slices: the bound comes from the slice's own values
+    bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
+    tau = topk_collect16(row, sc, bm, k, s);
+    LUMEN_TICK("topk_sampled", b);
+    if ((a.debug_stop >> 8) == 1u) return;
+  } else {
+    const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
+    tau = sample_threshold(row, V, target, s);
+    LUMEN_TICK("topk_sampled", b);
+    if ((a.debug_stop >> 8) == 1u) return;
+    bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
+    if (threadIdx.x == 0) s.cnt = 0;
+    __syncthreads();
+    range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
+      const uint32_t kk = tkey(v);
+      const bool in = kk >= tau && !(pen && bm_test(bm, i - sc.lo));
+      list_push(s.A, &s.cnt, in, ((uint64_t)(~kk) << 32) | i);
+    });
+  }
   if (pen) {
     const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
     for (uint32_t base = h0; base < h1; base += kThreads) {
