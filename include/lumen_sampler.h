@@ -135,6 +135,13 @@ typedef struct {
     uint32_t *tokens;                   /* device, [batch] output */
     lumen_row_trace *trace;             /* device, [batch] or NULL */
     float *penalized_out;               /* device, [batch][vocab] or NULL (debug) */
+    /* Device-resident RNG (the decode-loop form of `rng`, sampling.rs:1004):
+     * the Xorshift64 state of each row in device memory. When non-NULL (and
+     * uniforms_dev is NULL) the kernel draws next_f32 from rng_states_dev[b]
+     * for every row with temperature > 0 and vocab > 0, and stores the
+     * advanced state back; greedy rows leave their state untouched. No host
+     * draw and no staging copy per call. */
+    uint64_t *rng_states_dev;           /* device, [batch] in/out; may be NULL */
 } lumen_batch;
 
 /* Context: loads the gfx950 code object on `device`. The code object is
@@ -154,6 +161,14 @@ int lumen_sampler_sample_batch(lumen_sampler *s, const lumen_batch *batch, lumen
  * engine.rs:80-88) for a batch. */
 int lumen_sampler_sample_batch_sync(lumen_sampler *s, const lumen_batch *batch,
                                     uint32_t *tokens_host, lumen_stream stream);
+
+/* Range checks of the server's wire layer
+ * (crates/lumen-server/src/wire/openai.rs:357-381): temperature must be
+ * finite and in [0, 2], top_p finite and in [0, 1]. Returns LUMEN_OK or LUMEN_ERR_INVALID, and
+ * lumen_sampler_last_error() names the field. The sampler itself does not
+ * call it: like sample_logits, it accepts any value and skips a stage whose
+ * parameter is out of its active range (sampling.rs:493, 503, 511). */
+int lumen_sampling_params_validate(const lumen_sampling_params *p);
 
 /* Reference RNG (sampling.rs:45-106): Xorshift64 seeded through the
  * SplitMix64 finalizer. */

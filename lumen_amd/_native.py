@@ -34,6 +34,7 @@ EXPORTS = (
     "lumen_xorshift64_next_f32",
     "lumen_sampler_version",
     "lumen_sampler_last_error",
+    "lumen_sampling_params_validate",
 )
 
 
@@ -94,6 +95,7 @@ class BatchC(ctypes.Structure):
         ("tokens", ctypes.c_void_p),
         ("trace", ctypes.c_void_p),
         ("penalized_out", ctypes.c_void_p),
+        ("rng_states_dev", ctypes.c_void_p),
     ]
 
 
@@ -131,6 +133,8 @@ def load():
     L.lumen_sampler_version.argtypes = []
     L.lumen_sampler_last_error.restype = ctypes.c_char_p
     L.lumen_sampler_last_error.argtypes = []
+    L.lumen_sampling_params_validate.restype = ctypes.c_int
+    L.lumen_sampling_params_validate.argtypes = [ctypes.POINTER(SamplingParamsC)]
     _lib = L
     return L
 

@@ -119,6 +119,10 @@ struct KernelArgs {
   // synchronization. NULL otherwise.
   uint32_t* tokens_mapped;
   uint32_t* done_mapped;
+  // Device RNG: when non-NULL the draw of a sampled row is next_f32 of
+  // rng_dev[b] (Xorshift64, sampling.rs:74-104), and the row's finisher
+  // stores the advanced state.
+  uint64_t* rng_dev;
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };

@@ -276,6 +276,17 @@ const char* lumen_sampler_version(void) { return "lumen_sampler 0.1.0 gfx950"; }
 
 const char* lumen_sampler_last_error(void) { return g_last_error; }
 
+int lumen_sampling_params_validate(const lumen_sampling_params* p) {
+  if (!p) return fail(LUMEN_ERR_INVALID, "null params");
+  const float t = p->temperature, q = p->top_p;
+  // crates/lumen-server/src/wire/openai.rs:361-378: NaN and infinities fail the range test too
+  if (!std::isfinite(t) || !(t >= 0.0f && t <= 2.0f))
+    return fail(LUMEN_ERR_INVALID, "temperature must be between 0 and 2");
+  if (!std::isfinite(q) || !(q >= 0.0f && q <= 1.0f))
+    return fail(LUMEN_ERR_INVALID, "top_p must be between 0 and 1");
+  return LUMEN_OK;
+}
+
 int lumen_sampler_create(lumen_sampler** out, int device) {
   if (!out) return LUMEN_ERR_INVALID;
   *out = nullptr;
@@ -373,7 +384,9 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     return fail(LUMEN_ERR_INVALID, "dtype must be LUMEN_DTYPE_F32 or LUMEN_DTYPE_BF16");
   if (V > 0 && (!bt->logits || bt->row_stride < V))
     return fail(LUMEN_ERR_INVALID, "logits missing or row_stride < vocab");
-  if (!bt->uniforms && !bt->rng_states && !bt->uniforms_dev) {
+  // draws made on the device: caller-resident uniforms, or the device RNG
+  const bool dev_draws = bt->uniforms_dev || bt->rng_states_dev;
+  if (!bt->uniforms && !bt->rng_states && !dev_draws) {
     for (uint32_t b = 0; b < B; ++b)
       if (bt->params[b].temperature > 0.0f)
         return fail(LUMEN_ERR_INVALID, "sampled rows need uniforms or rng_states");
@@ -410,7 +423,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       count_window(s, bt->history + h0, h1 - h0, p.repeat_last_n);
     s->offs[b + 1] = (uint32_t)s->ids.size();
     any_pen |= (rows[b].flags & lumen::kPen) != 0;
-    if (V > 0 && !bt->uniforms_dev && !(rows[b].flags & lumen::kGreedy)) {
+    if (V > 0 && !dev_draws && !(rows[b].flags & lumen::kGreedy)) {
       // exactly one draw per sampled row (sampling.rs:1004)
       draws[b] = bt->rng_states ? lumen_xorshift64_next_f32(&bt->rng_states[b]) : bt->uniforms[b];
     }
@@ -490,7 +503,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   const size_t off_cnts = off_ids + (host_csr ? sizeof(uint32_t) * s->ids.size() : 0);
   const size_t off_map = a16(off_cnts + (host_csr ? sizeof(uint32_t) * s->cnts.size() : 0));
   const size_t static_sz = a16(off_map + sizeof(uint32_t) * s->blk_map.size());
-  const bool draw_block = !bt->uniforms_dev && !inl;
+  const bool draw_block = !dev_draws && !inl;
   const size_t total = static_sz + (draw_block ? sizeof(float) * B : 0);
   if (inl) {
     ka.inline_rows = B;
@@ -498,6 +511,8 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   }
   if (bt->uniforms_dev) {
     ka.uniforms = bt->uniforms_dev;
+  } else if (bt->rng_states_dev) {
+    ka.rng_dev = bt->rng_states_dev;
   } else if (inl) {
     ka.inline_draws = 1;
     for (uint32_t b = 0; b < B; ++b) ka.inline_uniforms[b] = draws[b];

@@ -795,6 +795,22 @@ __device__ __forceinline__ Row make_row(const KernelArgs& a, int b) {
   return row;
 }
 
+// Xorshift64::next_u64 / next_f32 (sampling.rs:90-104): x ^= x << 13,
+// x ^= x >> 7, x ^= x << 17; the draw is the top 24 bits times 2^-24.
+__device__ __forceinline__ uint64_t xorshift_step(uint64_t x) {
+  x ^= x << 13;
+  x ^= x >> 7;
+  x ^= x << 17;
+  return x;
+}
+
+// The draw of row b: a caller uniform, or next_f32 of the row's device RNG
+// state (not advanced here: the row's finisher stores the advanced state).
+__device__ __forceinline__ float row_draw(const KernelArgs& a, int b) {
+  if (a.rng_dev) return (float)(xorshift_step(a.rng_dev[b]) >> 40) * 0x1.0p-24f;
+  return a.inline_draws ? a.inline_uniforms[b] : a.uniforms[b];
+}
+
 __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrace& tr) {
   LUMEN_TICK("write", b);
   LUMEN_TICK_DUMP(b);
@@ -803,6 +819,11 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
     if (a.trace) {
       tr.token = token;
       a.trace[b] = tr;
+    }
+    if (a.rng_dev) {
+      // exactly one draw per sampled row with a non-empty vocabulary
+      const RowParams& P = a.inline_rows ? a.inline_params[b] : a.params[b];
+      if (!(P.flags & kGreedy) && a.vocab > 0) a.rng_dev[b] = xorshift_step(a.rng_dev[b]);
     }
     if (a.tokens_mapped) {
       a.tokens_mapped[b] = token;
@@ -1253,7 +1274,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
     return;
   }
 
-  const float rdraw = a.inline_draws ? a.inline_uniforms[b] : a.uniforms[b];
+  const float rdraw = row_draw(a, b);
   bool small = false;   // survivors in s.A as (idx << 32) | key, ascending idx
   uint32_t nlist = 0;
   bool topp_done = false;
@@ -1755,7 +1776,7 @@ __device__ __forceinline__ void slice_pen_out(const KernelArgs& a, int b, const 
 // path function (so the kernel entry passes only scalars to it).
 #define ROW_CONTEXT(a, b)                                                             \
   const RowParams P = (a).inline_rows ? (a).inline_params[b] : (a).params[b];         \
-  const float rdraw = (a).inline_draws ? (a).inline_uniforms[b] : (a).uniforms[b];    \
+  const float rdraw = row_draw((a), (b));                                             \
   RowWs& ws = (a).ws[b];                                                              \
   uint64_t* cand = (a).cand + (uint64_t)(b) * kCandCap;                               \
   const Row row = make_row((a), (b));                                                 \

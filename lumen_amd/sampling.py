@@ -47,6 +47,15 @@ class SamplingParams:
         return bool(abs(np.float32(rep - np.float32(1.0))) >= np.float32(F32_EPSILON)
                     or presence != 0.0 or freq != 0.0)
 
+    def validate(self) -> None:
+        """Wire-level range check (crates/lumen-server/src/wire/openai.rs:357-381)
+        through the library: temperature finite in [0, 2], top_p finite in
+        [0, 1] (None passes). Raises ValueError with the reference's message."""
+        c = self.to_c()
+        L = _native.load()
+        if L.lumen_sampling_params_validate(ctypes.byref(c)) != 0:
+            raise ValueError(L.lumen_sampler_last_error().decode(errors="replace"))
+
     def to_c(self) -> _native.SamplingParamsC:
         return _native.SamplingParamsC(
             float(self.temperature),
@@ -145,14 +154,16 @@ class Engine:
                      uniforms: Optional[Sequence[float]] = None,
                      rngs: Optional[Sequence[Xorshift64]] = None,
                      penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
-                     sync: bool = True, stream=None, uniforms_dev=None):
+                     sync: bool = True, stream=None, uniforms_dev=None, rng_states_dev=None):
         """Samples every row of `logits` [B, V].
 
         histories: SamplerState.history per row (the window is applied here),
         or penalty_counts = (offsets, ids, counts) device int32 tensors already
         windowed (the caller-resident SamplerState.freq).
         uniforms: one draw per row; or rngs: Xorshift64 per row (advanced);
-        or uniforms_dev: a float32 device tensor of draws (no staging copy).
+        or uniforms_dev: a float32 device tensor of draws (no staging copy);
+        or rng_states_dev: an int64 device tensor of Xorshift64 states, drawn
+        from and advanced by the kernel (greedy rows keep their state).
         Returns the token tensor (device); with sync=True also a host list.
         """
         import torch
@@ -186,6 +197,12 @@ class Engine:
             bt.history = flat.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
         if uniforms_dev is not None:
             bt.uniforms_dev = uniforms_dev.data_ptr()
+        elif rng_states_dev is not None:
+            if rng_states_dev.numel() < B or rng_states_dev.element_size() != 8 \
+                    or not rng_states_dev.is_contiguous() or rng_states_dev.device != lg.device:
+                raise ValueError("rng_states_dev: a contiguous 8-byte tensor of B states "
+                                 "on the logits' device")
+            bt.rng_states_dev = rng_states_dev.data_ptr()
         elif rngs is not None:
             st = np.array([r.state() for r in rngs], dtype=np.uint64)
             keep.append(st)
@@ -209,7 +226,7 @@ class Engine:
             rc = L.lumen_sampler_sample_batch_sync(self._h, ctypes.byref(bt), host, s)
         else:
             rc = L.lumen_sampler_sample_batch(self._h, ctypes.byref(bt), s)
-        if rngs is not None and uniforms_dev is None:
+        if rngs is not None and uniforms_dev is None and rng_states_dev is None:
             for r, v in zip(rngs, st.tolist()):
                 r.set_state(int(v))
         _native.check(rc, "lumen_sampler_sample_batch")

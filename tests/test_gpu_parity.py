@@ -321,3 +321,36 @@ def test_config2_sequential_draws(eng):
         rep = parity.compare(eng, lg, w.params, [hist], u, check_pen=True)
         assert_clean(rep, f"config2 draw {d}")
         hist = np.append(hist, np.uint32(rep["gpu"][0]))
+
+
+def test_device_rng_states(eng):
+    # rng_states_dev: the kernel draws Xorshift64::next_f32 (sampling.rs:45-106)
+    # from each row's device-resident state and stores the advanced state;
+    # greedy rows (temperature 0) keep theirs. Three calls in a row must give
+    # the tokens that host-side draws from the same streams give, and the
+    # states must equal the host generators' afterwards.
+    import torch
+    from lumen_amd.sampling import Xorshift64
+
+    B, V = 24, 5000
+    rng = np.random.default_rng(11)
+    lg = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    params = [SP(temperature=0.0) if b % 4 == 0 else
+              SP(temperature=0.8, top_p=0.9, top_k=50 if b % 3 else None) for b in range(B)]
+    seeds = [1000 + 7 * b for b in range(B)]
+    host = [Xorshift64(s) for s in seeds]
+    dev = torch.tensor([np.int64(np.uint64(h.state()).view(np.int64)) for h in host],
+                       dtype=torch.int64, device="cuda:0")
+    x = torch.from_numpy(lg).to("cuda:0")
+    for call in range(3):
+        log(f"case device_rng call {call} B={B} V={V}")
+        want = [0] * B
+        u = np.zeros(B, np.float32)
+        for b in range(B):
+            if params[b].temperature > 0:
+                u[b] = host[b].next_f32()
+        _, want = eng.sample_batch(x, params, uniforms=u)
+        _, got = eng.sample_batch(x, params, rng_states_dev=dev)
+        assert got == want, f"call {call}: {got} vs {want}"
+        st = dev.cpu().numpy().view(np.uint64)
+        assert [int(v) for v in st] == [h.state() for h in host], f"call {call} states"

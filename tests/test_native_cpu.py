@@ -68,11 +68,39 @@ def test_python_mirror_rng_and_params():
     assert SamplingParams(presence_penalty=0.5).penalties_active() is True
 
 
+def test_params_validate_wire_ranges():
+    # crates/lumen-server/src/wire/openai.rs:357-381: the closed ranges
+    # [0, 2] and [0, 1] with both ends accepted; NaN, infinities and any
+    # value just outside rejected, with the field named in the message
+    from lumen_amd.sampling import SamplingParams
+
+    f32 = np.float32
+    ok_t = [0.0, 1e-30, 1.0, 2.0, float(np.nextafter(f32(2.0), f32(0.0)))]
+    bad_t = [float("nan"), float("inf"), -float("inf"), -1e-30,
+             float(np.nextafter(f32(2.0), f32(3.0))), 2.5, -1.0]
+    ok_p = [None, 0.0, 0.5, 1.0]
+    bad_p = [float("nan"), float("inf"), -1e-30, float(np.nextafter(f32(1.0), f32(2.0))), 1.5]
+    for t in ok_t:
+        for q in ok_p:
+            SamplingParams(temperature=t, top_p=q).validate()
+    for t in bad_t:
+        with pytest.raises(ValueError, match="temperature must be between 0 and 2"):
+            SamplingParams(temperature=t).validate()
+    for q in bad_p:
+        with pytest.raises(ValueError, match="top_p must be between 0 and 1"):
+            SamplingParams(temperature=1.0, top_p=q).validate()
+    # temperature is checked first, as in the reference
+    with pytest.raises(ValueError, match="temperature"):
+        SamplingParams(temperature=3.0, top_p=3.0).validate()
+    L = _native.load()
+    assert L.lumen_sampling_params_validate(None) != 0
+
+
 def test_struct_layouts():
     # lumen_sampling_params: 6 floats, 2 u64, 2 i32 = 48 bytes
     assert ctypes.sizeof(_native.SamplingParamsC) == 48
     assert ctypes.sizeof(_native.RowTraceC) == 64
-    assert ctypes.sizeof(_native.BatchC) == 128
+    assert ctypes.sizeof(_native.BatchC) == 136
 
 
 def test_create_without_gpu_fails_cleanly():
