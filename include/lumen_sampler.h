@@ -72,7 +72,8 @@ typedef struct {
 
 /* Per-row diagnostics (optional). */
 typedef struct {
-    uint32_t status;           /* 0 ok; 1 tie overflow; 2 internal list overflow */
+    uint32_t status;           /* 0 ok; 1 tie overflow; 2 internal list overflow;
+                                  3 device history window longer than the ring */
     uint32_t path;             /* bit0 greedy, bit1 LDS path, bit2 streaming path,
                                   bit3 uniform top-p, bit4 uniform final, bit5 NaN */
     uint32_t topk_cutoff_key;  /* f32::total_cmp key of the k-th largest logit */
@@ -142,6 +143,21 @@ typedef struct {
      * advanced state back; greedy rows leave their state untouched. No host
      * draw and no staging copy per call. */
     uint64_t *rng_states_dev;           /* device, [batch] in/out; may be NULL */
+    /* Penalty window, form C (device-resident history, the decode-loop form
+     * of SamplerState, sampling.rs:353-389): hist_ring_dev holds the last
+     * hist_cap tokens of each row ([batch][hist_cap], the k-th recorded token
+     * of row b at k % hist_cap) and hist_len_dev[b] counts the tokens
+     * recorded. The library counts each row's window on the device
+     * (repeat_last_n, or the whole history when it is 0) and, after
+     * sampling, records the row's token (SamplerState::record) -- every row
+     * with vocab > 0 and a token other than LUMEN_TOKEN_ERROR. A window
+     * longer than hist_cap cannot be counted: that row's token is
+     * LUMEN_TOKEN_ERROR with trace status 3. 1 <= hist_cap <= 8192. Excludes
+     * forms A and B. */
+    uint32_t *hist_ring_dev;            /* device, [batch][hist_cap] in/out; may be NULL */
+    uint32_t *hist_len_dev;             /* device, [batch] in/out */
+    uint32_t hist_cap;
+    uint32_t reserved0;
 } lumen_batch;
 
 /* Context: loads the gfx950 code object on `device`. The code object is

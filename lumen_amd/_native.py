@@ -96,6 +96,10 @@ class BatchC(ctypes.Structure):
         ("trace", ctypes.c_void_p),
         ("penalized_out", ctypes.c_void_p),
         ("rng_states_dev", ctypes.c_void_p),
+        ("hist_ring_dev", ctypes.c_void_p),
+        ("hist_len_dev", ctypes.c_void_p),
+        ("hist_cap", ctypes.c_uint32),
+        ("reserved0", ctypes.c_uint32),
     ]
 
 

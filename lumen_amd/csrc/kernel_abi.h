@@ -17,7 +17,8 @@ struct RowParams {
   float freq;         // frequency penalty
   uint32_t top_k;     // used iff kTopK; 1 <= top_k < V
   uint32_t flags;
-  uint32_t pad[3];
+  uint32_t window;    // repeat_last_n clipped to 32 bits; 0 = the whole history (sampling.rs:864)
+  uint32_t pad[2];
 };
 
 enum RowFlags : uint32_t {
@@ -53,7 +54,14 @@ enum RowStatus : uint32_t {
   kStatusOk = 0,
   kStatusTieOverflow = 1,   // > list capacity of exactly-equal keys in one top-p window
   kStatusListOverflow = 2,  // internal: window larger than planned
+  kStatusHistOverflow = 3,  // device history: the penalty window is longer than the ring
 };
+
+// Device history rings hold at most this many tokens per row (the window
+// counts are built in an LDS hash table of twice as many slots).
+constexpr uint32_t kRingMaxCap = 8192;
+constexpr uint32_t kHistBad = 0xffffffffu;
+constexpr uint32_t kTokenError = 0xffffffffu;  // LUMEN_TOKEN_ERROR  // hist_end value of a row whose window overflowed
 
 constexpr int kInlineRows = 8;
 constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
@@ -88,7 +96,8 @@ struct KernelArgs {
   int32_t dtype;             // 0 = f32, 1 = bf16
   uint32_t pad0;
   const RowParams* params;   // [B] device
-  const uint32_t* hist_off;  // [B+1] offsets into hist_ids / hist_cnt
+  const uint32_t* hist_off;  // [B+1] offsets into hist_ids / hist_cnt (row b ends at
+                             // hist_off[b + 1], or at hist_end[b] when hist_end is set)
   const uint32_t* hist_ids;  // unique token ids of the penalty window, per row
   const uint32_t* hist_cnt;  // occurrence counts
   const float* uniforms;     // [B] draw per row (ignored by greedy rows)
@@ -123,6 +132,16 @@ struct KernelArgs {
   // rng_dev[b] (Xorshift64, sampling.rs:74-104), and the row's finisher
   // stores the advanced state.
   uint64_t* rng_dev;
+  // Device history: a ring of the last ring_cap tokens of each row
+  // ([B][ring_cap], token k of row b at k % ring_cap) and the count of tokens
+  // recorded (ring_len[b]). lumen_hist_window builds the penalty window's
+  // counts from it into hist_off / hist_ids / hist_cnt (a region of ring_cap
+  // entries per row) and hist_end; the finisher of each row records its token.
+  uint32_t* ring;
+  uint32_t* ring_len;
+  uint32_t* hist_end;        // [B] end of row b's counts (hist_off[b] = kHistBad on overflow)
+  uint32_t ring_cap;
+  uint32_t pad2;
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };

@@ -127,6 +127,7 @@ struct lumen_sampler {
   int device = 0;
   hipModule_t module = nullptr;
   hipFunction_t fn = nullptr;
+  hipFunction_t fn_hist = nullptr;  // lumen_hist_window
   // staging: one pinned host block and one device block, same layout
   void* pin = nullptr;
   size_t pin_cap = 0;
@@ -136,6 +137,7 @@ struct lumen_sampler {
   DevBuf cand;  // [B][kCandCap] candidate buffers
   DevBuf est;   // [B][kRowRecs][kRecWords] run records of the split top-p path
   DevBuf hist;  // [B][kMaxSlices][kMassBins] candidate mass histograms
+  DevBuf wcnt;  // device history: [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts
   int cu_count = 0;
   int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
   hipEvent_t staged = nullptr;  // recorded after the last staging copy
@@ -200,6 +202,7 @@ int resolve_row(const lumen_sampling_params& p, uint32_t V, bool has_window, Row
   // penalties_active (sampling.rs:332-337); apply_penalties returns early on
   // an empty history (:858)
   const bool pen = std::fabs(rep - 1.0f) >= kF32Eps || pres != 0.0f || freq != 0.0f;
+  r.window = p.repeat_last_n > 0xffffffffull ? 0xffffffffu : (uint32_t)p.repeat_last_n;
   r.rep = rep;
   r.presence = pres;
   r.freq = freq;
@@ -323,7 +326,8 @@ int lumen_sampler_create(lumen_sampler** out, int device) {
     delete s;
     return LUMEN_ERR_CODE_OBJECT;
   }
-  if (hipModuleGetFunction(&s->fn, s->module, "lumen_sample_rows") != hipSuccess) {
+  if (hipModuleGetFunction(&s->fn, s->module, "lumen_sample_rows") != hipSuccess ||
+      hipModuleGetFunction(&s->fn_hist, s->module, "lumen_hist_window") != hipSuccess) {
     (void)hipGetLastError();
     (void)hipModuleUnload(s->module);
     delete s;
@@ -395,6 +399,14 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     return fail(LUMEN_ERR_INVALID, "pen_offsets needs pen_ids and pen_counts");
   if (bt->history_offsets && !bt->history && bt->history_offsets[B] > 0)
     return fail(LUMEN_ERR_INVALID, "history_offsets without history");
+  const bool ring = bt->hist_ring_dev != nullptr;
+  if (ring) {
+    if (!bt->hist_len_dev) return fail(LUMEN_ERR_INVALID, "hist_ring_dev needs hist_len_dev");
+    if (bt->hist_cap == 0 || bt->hist_cap > lumen::kRingMaxCap)
+      return fail(LUMEN_ERR_INVALID, "hist_cap must be between 1 and 8192");
+    if (bt->pen_offsets || bt->history_offsets)
+      return fail(LUMEN_ERR_INVALID, "hist_ring_dev excludes history_offsets and pen_offsets");
+  }
   DeviceGuard g(s->device);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 
@@ -409,7 +421,9 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     const lumen_sampling_params& p = bt->params[b];
     bool has_window = false;
     uint64_t h0 = 0, h1 = 0;
-    if (!bt->pen_offsets && bt->history_offsets) {
+    if (ring) {
+      has_window = true;  // counted on the device; an empty window applies nothing
+    } else if (!bt->pen_offsets && bt->history_offsets) {
       h0 = bt->history_offsets[b];
       h1 = bt->history_offsets[b + 1];
       if (h1 < h0) return fail(LUMEN_ERR_INVALID, "history_offsets must be non-decreasing");
@@ -419,7 +433,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     }
     int rc = resolve_row(p, V, has_window, rows[b]);
     if (rc != LUMEN_OK) return fail(rc, "anti_restate is not supported on the GPU path");
-    if (!bt->pen_offsets && (rows[b].flags & lumen::kPen))
+    if (!bt->pen_offsets && !ring && (rows[b].flags & lumen::kPen))
       count_window(s, bt->history + h0, h1 - h0, p.repeat_last_n);
     s->offs[b + 1] = (uint32_t)s->ids.size();
     any_pen |= (rows[b].flags & lumen::kPen) != 0;
@@ -496,7 +510,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   //   draw block   [uniforms]: copied every call unless the draws are inline
   //                kernel arguments or already in device memory.
   const bool inl = B <= (uint32_t)lumen::kInlineRows;
-  const bool host_csr = !bt->pen_offsets;
+  const bool host_csr = !bt->pen_offsets && !ring;
   auto a16 = [](size_t x) { return (x + 15) & ~size_t(15); };
   const size_t off_offs = inl ? 0 : a16(sizeof(RowParams) * B);
   const size_t off_ids = off_offs + (host_csr ? sizeof(uint32_t) * (B + 1) : 0);
@@ -569,7 +583,19 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       ka.hist_cnt = reinterpret_cast<const uint32_t*>(dp + off_cnts);
     }
   }
-  if (!host_csr) {
+  if (ring) {
+    const size_t cap = bt->hist_cap;
+    int rc = ensure_dev(s->wcnt, sizeof(uint32_t) * (2 * B + 2 * cap * B));
+    if (rc != LUMEN_OK) return rc;
+    uint32_t* w = static_cast<uint32_t*>(s->wcnt.p);
+    ka.hist_off = w;
+    ka.hist_end = w + B;
+    ka.hist_ids = w + 2 * B;
+    ka.hist_cnt = w + 2 * B + cap * B;
+    ka.ring = bt->hist_ring_dev;
+    ka.ring_len = bt->hist_len_dev;
+    ka.ring_cap = bt->hist_cap;
+  } else if (!host_csr) {
     ka.hist_off = bt->pen_offsets;
     ka.hist_ids = bt->pen_ids;
     ka.hist_cnt = bt->pen_counts;
@@ -580,6 +606,16 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     if (rc != LUMEN_OK) return rc;
     ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
     ka.pen_stride = stride;
+  }
+  ka.tokens_mapped = tok_map;
+  ka.done_mapped = done_map;
+  if (ring) {
+    // the window counts of every row, ahead of the sampler on the same stream
+    size_t hsz = sizeof(ka);
+    void* hcfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &hsz,
+                    HIP_LAUNCH_PARAM_END};
+    hipError_t e = hipModuleLaunchKernel(s->fn_hist, B, 1, 1, 1024, 1, 1, 0, st, nullptr, hcfg);
+    if (e != hipSuccess) return hip_fail(e);
   }
   if (G > 1) {
     const size_t ws_bytes = sizeof(lumen::RowWs) * B;
@@ -610,8 +646,6 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       return hip_fail(e);
     }
   }
-  ka.tokens_mapped = tok_map;
-  ka.done_mapped = done_map;
   size_t argsz = sizeof(ka);
   void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &ka, HIP_LAUNCH_PARAM_BUFFER_SIZE, &argsz,
                  HIP_LAUNCH_PARAM_END};

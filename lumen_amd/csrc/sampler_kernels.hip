@@ -811,10 +811,27 @@ __device__ __forceinline__ float row_draw(const KernelArgs& a, int b) {
   return a.inline_draws ? a.inline_uniforms[b] : a.uniforms[b];
 }
 
+// End of row b's penalty counts (hist_off[b] is the start).
+__device__ __forceinline__ uint32_t hist_hi(const KernelArgs& a, int b) {
+  return a.hist_end ? a.hist_end[b] : a.hist_off[b + 1];
+}
+
 __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_t token, RowTrace& tr) {
   LUMEN_TICK("write", b);
   LUMEN_TICK_DUMP(b);
   if (threadIdx.x == 0) {
+    if (a.ring) {
+      if (a.hist_off[b] == kHistBad) {
+        // the penalty window did not fit the ring (lumen_hist_window)
+        token = kTokenError;
+        tr.status = kStatusHistOverflow;
+      } else if (token != kTokenError) {
+        // SamplerState::record (sampling.rs:381-384) into the device ring
+        const uint32_t n = a.ring_len[b];
+        a.ring[(uint64_t)b * a.ring_cap + n % a.ring_cap] = token;
+        a.ring_len[b] = n + 1u;
+      }
+    }
     a.tokens[b] = token;
     if (a.trace) {
       tr.token = token;
@@ -1240,7 +1257,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   Row row = make_row(a, b);
 
   // ---- penalties: materialize the penalized row (sampling.rs:850-879) ----
-  const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+  const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
   if ((P.flags & kPen) && h1 > h0) {
     float* dst = a.pen_scratch + (uint64_t)b * a.pen_stride;
     row_foreach(row, [&](uint32_t i, float v) { dst[i] = v; });
@@ -1743,7 +1760,7 @@ __device__ __forceinline__ uint32_t* slice_bitmap(const KernelArgs& a, int b, Sl
   const uint32_t nw = (sc.hi - sc.lo + 31u) / 32u;
   for (uint32_t i = threadIdx.x; i < nw; i += kThreads) bm[i] = 0u;
   __syncthreads();
-  const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+  const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
   for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
     uint32_t id = a.hist_ids[j];
     if (id >= sc.lo && id < sc.hi) atomicOr(&bm[(id - sc.lo) >> 5], 1u << ((id - sc.lo) & 31u));
@@ -1764,7 +1781,7 @@ __device__ __forceinline__ void slice_pen_out(const KernelArgs& a, int b, const 
   __threadfence();
   __syncthreads();
   if (pen) {
-    const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
     for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
       uint32_t id = a.hist_ids[j];
       if (id >= sc.lo && id < sc.hi) po[id] = penalize(row.at(id), a.hist_cnt[j], P);
@@ -1789,7 +1806,7 @@ __device__ __forceinline__ void greedy_split(const KernelArgs& a, int b, uint32_
   ROW_CONTEXT(a, b);
   const uint32_t V = a.vocab;
   const Slice sc = slice_bounds(V, G, sl);
-  const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
+  const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
   uint64_t best = 0;
@@ -1799,7 +1816,7 @@ __device__ __forceinline__ void greedy_split(const KernelArgs& a, int b, uint32_
     best = k > best ? k : best;
   });
   if (pen) {
-    const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
     for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
       uint32_t id = a.hist_ids[j];
       if (id >= sc.lo && id < sc.hi) {
@@ -1881,7 +1898,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   const uint32_t V = a.vocab;
   const uint32_t k = P.top_k;
   const Slice sc = slice_bounds(V, G, sl);
-  const bool pen = (P.flags & kPen) && a.hist_off[b + 1] > a.hist_off[b];
+  const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   LUMEN_TICK("topk_start", b);
   if ((a.debug_stop >> 8) == 15u) return;
@@ -1908,7 +1925,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     });
   }
   if (pen) {
-    const uint32_t h0 = a.hist_off[b], h1 = a.hist_off[b + 1];
+    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
     for (uint32_t base = h0; base < h1; base += kThreads) {
       const uint32_t j = base + threadIdx.x;
       bool in = false;
@@ -2728,6 +2745,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
   uint32_t b, sl, G;
   block_row(a, b, sl, G);
   if (b >= a.batch) return;
+
   LUMEN_TICK_SLOT(b, sl);
   __syncthreads();
   if (G == 1u) {
@@ -2751,5 +2769,84 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
     }
   }
   row_reset(a, b, s);
+}
+
+// Penalty window counts from the device history ring, one workgroup per row
+// (sampling.rs:858-878: the last `window` tokens, or the whole history when
+// window is 0, counted per distinct id). Runs before lumen_sample_rows on the
+// same stream. Counts go through an LDS hash table (2 * kRingMaxCap slots,
+// linear probing), then out as (id, count) pairs in slot order, which the
+// sampler does not depend on. A window longer than the ring cannot be
+// counted: hist_off[b] = kHistBad (an empty range, since hist_end[b] is
+// below it) and the row's token becomes LUMEN_TOKEN_ERROR with
+// kStatusHistOverflow when it is written.
+constexpr uint32_t kHashSlots = 2u * kRingMaxCap;
+constexpr uint32_t kHashEmpty = 0xffffffffu;
+static_assert(kHashSlots == (1u << 14), "the hash takes the top 14 bits");
+
+extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs args) {
+  (void)args;
+  const KernelArgs& a =
+      *reinterpret_cast<const KernelArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+  __shared__ uint32_t hkey[kHashSlots];
+  __shared__ uint32_t hcnt[kHashSlots];
+  __shared__ uint32_t nout;
+  const uint32_t b = blockIdx.x, t = threadIdx.x;
+  if (b >= a.batch) return;
+  const RowParams& P = a.inline_rows ? a.inline_params[b] : a.params[b];
+  const uint32_t cap = a.ring_cap;
+  const uint32_t base = b * cap;
+  uint32_t* off = const_cast<uint32_t*>(a.hist_off);
+  uint32_t* ids = const_cast<uint32_t*>(a.hist_ids);
+  uint32_t* cnt = const_cast<uint32_t*>(a.hist_cnt);
+  const uint32_t len = a.ring_len[b];
+  const uint32_t w = (P.window > 0u && P.window < len) ? P.window : len;
+  if (!(P.flags & kPen) || w == 0u) {
+    if (t == 0) {
+      off[b] = base;
+      a.hist_end[b] = base;
+    }
+    return;
+  }
+  if (w > cap) {
+    // no counts (an empty range); the row's finisher reports the overflow
+    if (t == 0) {
+      off[b] = kHistBad;
+      a.hist_end[b] = base;
+    }
+    return;
+  }
+  for (uint32_t i = t; i < kHashSlots; i += blockDim.x) {
+    hkey[i] = kHashEmpty;
+    hcnt[i] = 0u;
+  }
+  if (t == 0) nout = 0u;
+  __syncthreads();
+  const uint32_t* ring = a.ring + (uint64_t)base;
+  for (uint32_t j = t; j < w; j += blockDim.x) {
+    const uint32_t id = ring[(len - w + j) % cap];
+    uint32_t h = (id * 2654435761u) >> (32 - 14);  // Fibonacci hashing into 2^14 slots
+    for (;;) {
+      const uint32_t old = atomicCAS(&hkey[h], kHashEmpty, id);
+      if (old == kHashEmpty || old == id) {
+        atomicAdd(&hcnt[h], 1u);
+        break;
+      }
+      h = (h + 1u) & (kHashSlots - 1u);
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = t; i < kHashSlots; i += blockDim.x) {
+    if (hkey[i] != kHashEmpty) {
+      const uint32_t k = atomicAdd(&nout, 1u);
+      ids[base + k] = hkey[i];
+      cnt[base + k] = hcnt[i];
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    off[b] = base;
+    a.hist_end[b] = base + nout;
+  }
 }
 }  // namespace lumen

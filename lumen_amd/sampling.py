@@ -154,7 +154,8 @@ class Engine:
                      uniforms: Optional[Sequence[float]] = None,
                      rngs: Optional[Sequence[Xorshift64]] = None,
                      penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
-                     sync: bool = True, stream=None, uniforms_dev=None, rng_states_dev=None):
+                     sync: bool = True, stream=None, uniforms_dev=None, rng_states_dev=None,
+                     hist_ring_dev=None, hist_len_dev=None):
         """Samples every row of `logits` [B, V].
 
         histories: SamplerState.history per row (the window is applied here),
@@ -164,6 +165,9 @@ class Engine:
         or uniforms_dev: a float32 device tensor of draws (no staging copy);
         or rng_states_dev: an int64 device tensor of Xorshift64 states, drawn
         from and advanced by the kernel (greedy rows keep their state).
+        hist_ring_dev / hist_len_dev: device-resident history (an int32
+        [B, cap] ring and an int32 [B] count of recorded tokens); the window
+        is counted on the device and each row's token recorded there.
         Returns the token tensor (device); with sync=True also a host list.
         """
         import torch
@@ -195,6 +199,18 @@ class Engine:
             keep += [offs, flat]
             bt.history_offsets = offs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
             bt.history = flat.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+        if hist_ring_dev is not None:
+            if histories is not None or penalty_counts is not None:
+                raise ValueError("hist_ring_dev excludes histories and penalty_counts")
+            if hist_len_dev is None or hist_ring_dev.dim() != 2 or hist_ring_dev.shape[0] < B \
+                    or hist_ring_dev.element_size() != 4 or not hist_ring_dev.is_contiguous() \
+                    or hist_len_dev.element_size() != 4 or hist_len_dev.numel() < B \
+                    or hist_ring_dev.device != lg.device or hist_len_dev.device != lg.device:
+                raise ValueError("hist_ring_dev: a contiguous 4-byte [B, cap] tensor and "
+                                 "hist_len_dev a 4-byte [B] tensor on the logits' device")
+            bt.hist_ring_dev = hist_ring_dev.data_ptr()
+            bt.hist_len_dev = hist_len_dev.data_ptr()
+            bt.hist_cap = hist_ring_dev.shape[1]
         if uniforms_dev is not None:
             bt.uniforms_dev = uniforms_dev.data_ptr()
         elif rng_states_dev is not None:
@@ -231,6 +247,36 @@ class Engine:
                 r.set_state(int(v))
         _native.check(rc, "lumen_sampler_sample_batch")
         return (tokens_out, list(host)) if sync else (tokens_out, None)
+
+
+class DeviceDecodeState:
+    """Per-row decode state kept in device memory: the Xorshift64 state
+    (Sampler::rng, sampling.rs:395-403) and the history ring
+    (SamplerState::history, sampling.rs:353-389) of `cap` tokens. A decode
+    step samples with `step(engine, logits, params)`: no host draw, no
+    history upload, and the sampled tokens are recorded on the device."""
+
+    def __init__(self, seeds: Sequence[int], cap: int = 4096, device: int = 0,
+                 histories: Optional[Sequence[Sequence[int]]] = None):
+        import torch
+
+        B = len(seeds)
+        dev = torch.device("cuda", device)
+        st = np.array([Xorshift64(s).state() for s in seeds], dtype=np.uint64)
+        self.rng = torch.from_numpy(st.view(np.int64).copy()).to(dev)
+        ring = np.zeros((B, cap), dtype=np.uint32)
+        lens = np.zeros(B, dtype=np.uint32)
+        for b, h in enumerate(histories or []):
+            h = np.asarray(h, dtype=np.uint32).reshape(-1)
+            for k, tok in enumerate(h):
+                ring[b, k % cap] = tok
+            lens[b] = h.size
+        self.ring = torch.from_numpy(ring.view(np.int32)).to(dev)
+        self.lens = torch.from_numpy(lens.view(np.int32)).to(dev)
+
+    def step(self, eng: "Engine", logits, params: Sequence[SamplingParams], **kw):
+        return eng.sample_batch(logits, params, rng_states_dev=self.rng,
+                                hist_ring_dev=self.ring, hist_len_dev=self.lens, **kw)
 
 
 _engines: Dict[int, Engine] = {}

@@ -354,3 +354,94 @@ def test_device_rng_states(eng):
         assert got == want, f"call {call}: {got} vs {want}"
         st = dev.cpu().numpy().view(np.uint64)
         assert [int(v) for v in st] == [h.state() for h in host], f"call {call} states"
+
+
+def _decode_rows(B, rng):
+    params = []
+    for b in range(B):
+        k = b % 6
+        if k == 0:
+            params.append(SP(temperature=0.0, repetition_penalty=1.3, repeat_last_n=4))
+        elif k == 1:
+            params.append(SP(temperature=0.9, top_k=40, frequency_penalty=0.7))
+        elif k == 2:
+            params.append(SP(temperature=0.7, top_p=0.9, presence_penalty=0.5, repeat_last_n=3))
+        elif k == 3:
+            params.append(SP(temperature=1.1, repetition_penalty=1.2, min_p=0.05))
+        elif k == 4:
+            params.append(SP(temperature=0.8, top_p=0.95))
+        else:
+            params.append(SP(temperature=0.0, frequency_penalty=2.0))
+    return params
+
+
+@pytest.mark.parametrize("V", [600, 248320])
+def test_device_decode_state(eng, V):
+    # A decode loop with the history ring and the RNG states in device memory
+    # against the same loop driven from the host (SamplerState::history and
+    # Xorshift64 on the host, Sampler::sample at sampling.rs:429-433): every
+    # step's tokens must agree, and the ring must hold the tokens recorded.
+    import torch
+    from lumen_amd.sampling import DeviceDecodeState, Xorshift64
+
+    B = 12 if V < 10000 else 6
+    rng = np.random.default_rng(V)
+    params = _decode_rows(B, rng)
+    seeds = [900 + b for b in range(B)]
+    prompt = [rng.integers(0, V, size=int(rng.integers(0, 5))).astype(np.uint32) for _ in range(B)]
+    cap = 64
+    ds = DeviceDecodeState(seeds, cap=cap, histories=prompt)
+    host_rng = [Xorshift64(s) for s in seeds]
+    hist = [list(p) for p in prompt]
+    steps = 20 if V < 10000 else 6
+    for step in range(steps):
+        # logits that favour recently sampled ids, so the penalties matter
+        lg = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+        for b in range(B):
+            for tok in hist[b][-3:]:
+                lg[b, tok] += 4.0
+        x = torch.from_numpy(lg).to("cuda:0")
+        log(f"case device_decode V={V} step {step}")
+        _, want = eng.sample_batch(x, params, histories=[np.array(h, np.uint32) for h in hist],
+                                   rngs=host_rng)
+        _, got = ds.step(eng, x, params)
+        assert got == want, f"step {step}: {got} vs {want}"
+        for b in range(B):
+            hist[b].append(want[b])
+    lens = ds.lens.cpu().numpy()
+    ring = ds.ring.cpu().numpy().view(np.uint32)
+    for b in range(B):
+        assert lens[b] == len(hist[b])
+        for k in range(max(0, len(hist[b]) - cap), len(hist[b])):
+            assert ring[b, k % cap] == hist[b][k]
+    st = ds.rng.cpu().numpy().view(np.uint64)
+    assert [int(v) for v in st] == [r.state() for r in host_rng]
+
+
+def test_device_history_overflow(eng):
+    # a whole-history penalty window longer than the ring cannot be counted:
+    # that row reports an error (status 3) and the other rows are unaffected
+    import torch
+    from lumen_amd import _native
+    from lumen_amd.sampling import DeviceDecodeState
+
+    V = 300
+    params = [SP(temperature=0.0, repetition_penalty=1.5),
+              SP(temperature=0.0, repetition_penalty=1.5, repeat_last_n=8),
+              SP(temperature=0.0)]
+    hist = [list(range(20))] * 3
+    ds = DeviceDecodeState([1, 2, 3], cap=16, histories=hist)
+    lg = torch.from_numpy(np.random.default_rng(3).standard_normal((3, V)).astype(np.float32)).cuda()
+    tr = torch.zeros((3, 16), dtype=torch.int32, device="cuda:0")
+    toks, _ = ds.step(eng, lg, params, trace=tr, sync=False)
+    torch.cuda.synchronize()
+    t = toks.cpu().numpy().view(np.uint32)
+    st = tr.cpu().numpy()[:, 0]
+    assert t[0] == 0xFFFFFFFF and st[0] == 3
+    assert t[1] != 0xFFFFFFFF and st[1] == 0 and t[2] != 0xFFFFFFFF
+    _, want = eng.sample_batch(lg[1:], params[1:], histories=[np.array(h, np.uint32) for h in hist[1:]])
+    assert list(t[1:]) == want
+    lens = ds.lens.cpu().numpy()
+    assert list(lens) == [20, 21, 21]
+    with pytest.raises(RuntimeError):
+        ds.step(eng, lg, params)

@@ -100,7 +100,7 @@ def test_struct_layouts():
     # lumen_sampling_params: 6 floats, 2 u64, 2 i32 = 48 bytes
     assert ctypes.sizeof(_native.SamplingParamsC) == 48
     assert ctypes.sizeof(_native.RowTraceC) == 64
-    assert ctypes.sizeof(_native.BatchC) == 136
+    assert ctypes.sizeof(_native.BatchC) == 160
 
 
 def test_create_without_gpu_fails_cleanly():
