@@ -64,11 +64,20 @@ typedef struct {
     float frequency_penalty;
     uint64_t top_k;
     uint64_t repeat_last_n;
-    int32_t anti_restate;       /* greedy anti-degeneration guard; not supported on
-                                   the GPU path yet: rows that set it are rejected
-                                   with LUMEN_ERR_UNSUPPORTED */
+    int32_t anti_restate;       /* greedy anti-degeneration guard (sampling.rs:
+                                   472-474, 563-836); see lumen_batch.guard_out */
     int32_t reserved;
 } lumen_sampling_params;
+
+/* Token bytes for the anti-restate guard's sub-word rule -- the embedder's
+ * per-id byte decoder (SamplerState::decoder, sampling.rs:343-378) as a
+ * table: the bytes of id i are data[offsets[i] .. offsets[i + 1]); ids at or
+ * above `count` decode to no bytes. */
+typedef struct {
+    const uint8_t *data;
+    const uint64_t *offsets;            /* [count + 1] */
+    uint64_t count;
+} lumen_token_bytes;
 
 /* Per-row diagnostics (optional). */
 typedef struct {
@@ -158,6 +167,20 @@ typedef struct {
     uint32_t *hist_len_dev;             /* device, [batch] in/out */
     uint32_t hist_cap;
     uint32_t reserved0;
+    /* Greedy rows with anti_restate (sampling.rs:472-474). The device picks
+     * the guard's candidates: guard_out[b][0] = the raw argmax,
+     * guard_out[b][1..8] = the ids of the 8 largest finite penalized logits
+     * in (value desc, id asc) order (LUMEN_TOKEN_ERROR where fewer exist) --
+     * everything guarded_argmax (sampling.rs:563-603) can probe.
+     *   - sample_batch_sync applies the guard's rules itself
+     *     (lumen_anti_restate_select) with form-A histories and `decoder`,
+     *     and returns the guarded token on the host and in `tokens`;
+     *     guard_out may be NULL. Forms B and C are rejected for such rows
+     *     (LUMEN_ERR_UNSUPPORTED): the rules need the token sequence.
+     *   - sample_batch leaves the raw argmax in `tokens`; guard_out is then
+     *     required and the caller applies lumen_anti_restate_select. */
+    uint32_t *guard_out;                /* device, [batch][9] or NULL */
+    const lumen_token_bytes *decoder;   /* host, or NULL (sub-word rule off) */
 } lumen_batch;
 
 /* Context: loads the gfx950 code object on `device`. The code object is
@@ -185,6 +208,18 @@ int lumen_sampler_sample_batch_sync(lumen_sampler *s, const lumen_batch *batch,
  * call it: like sample_logits, it accepts any value and skips a stage whose
  * parameter is out of its active range (sampling.rs:493, 503, 511). */
 int lumen_sampling_params_validate(const lumen_sampling_params *p);
+
+/* The anti-restate guard's choice (guarded_argmax, sampling.rs:563-603)
+ * from the 9 candidates of lumen_batch.guard_out, the row's history
+ * (SamplerState::history, oldest first) and an optional decoder: probes the
+ * raw argmax, then the finite candidates in order, vetoing each that
+ * restates a sub-word (sampling.rs:732-780), closes a back-to-back repeat of
+ * a 3..8-token span (:819-836) or occurs 5+ times in the last 28 tokens
+ * (:693-701); at most 8 probes, else the raw argmax. The rules read
+ * LUMEN_ANTI_RESTATE_{SUBWORD,NGRAM,LOOP} once (0/false/no/off disables a
+ * rule, :625-662). */
+uint32_t lumen_anti_restate_select(const uint32_t *candidates, const uint32_t *history,
+                                   uint64_t history_len, const lumen_token_bytes *decoder);
 
 /* Reference RNG (sampling.rs:45-106): Xorshift64 seeded through the
  * SplitMix64 finalizer. */

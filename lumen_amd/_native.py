@@ -35,6 +35,7 @@ EXPORTS = (
     "lumen_sampler_version",
     "lumen_sampler_last_error",
     "lumen_sampling_params_validate",
+    "lumen_anti_restate_select",
 )
 
 
@@ -76,6 +77,14 @@ class RowTraceC(ctypes.Structure):
 TRACE_WORDS = ctypes.sizeof(RowTraceC) // 4
 
 
+class TokenBytesC(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("offsets", ctypes.c_void_p),
+        ("count", ctypes.c_uint64),
+    ]
+
+
 class BatchC(ctypes.Structure):
     _fields_ = [
         ("logits", ctypes.c_void_p),
@@ -100,6 +109,8 @@ class BatchC(ctypes.Structure):
         ("hist_len_dev", ctypes.c_void_p),
         ("hist_cap", ctypes.c_uint32),
         ("reserved0", ctypes.c_uint32),
+        ("guard_out", ctypes.c_void_p),
+        ("decoder", ctypes.POINTER(TokenBytesC)),
     ]
 
 
@@ -137,6 +148,10 @@ def load():
     L.lumen_sampler_version.argtypes = []
     L.lumen_sampler_last_error.restype = ctypes.c_char_p
     L.lumen_sampler_last_error.argtypes = []
+    L.lumen_anti_restate_select.restype = ctypes.c_uint32
+    L.lumen_anti_restate_select.argtypes = [ctypes.POINTER(ctypes.c_uint32),
+                                            ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint64,
+                                            ctypes.POINTER(TokenBytesC)]
     L.lumen_sampling_params_validate.restype = ctypes.c_int
     L.lumen_sampling_params_validate.argtypes = [ctypes.POINTER(SamplingParamsC)]
     _lib = L

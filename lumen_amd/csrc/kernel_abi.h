@@ -28,6 +28,7 @@ enum RowFlags : uint32_t {
   kTopK = 8u,     // 0 < k < V (sampling.rs:493)
   kTopP = 16u,    // 0 < p < 1 (sampling.rs:503)
   kMinP = 32u,    // min_p > 0 (sampling.rs:511)
+  kAnti = 64u,    // greedy with the anti-restate guard (sampling.rs:472-474): candidates out
 };
 
 // Per-row diagnostics (optional output), mirrors the oracle's trace.
@@ -86,7 +87,14 @@ struct RowWs {
   uint32_t part_nan[kMaxSlices];
   uint64_t part_arg[kMaxSlices];
   double part_e[kMaxSlices];
+  uint64_t part_top[kMaxSlices][8];  // anti-restate rows: each slice's 8 largest finite keys
 };
+
+// Anti-restate candidates per row: [0] the raw argmax (total_cmp over every
+// value, lowest index on ties), [1..8] the 8 largest finite values' ids in
+// (value desc, id asc) order, kGuardNone where fewer exist.
+constexpr int kGuardWords = 9;
+constexpr uint32_t kGuardNone = 0xffffffffu;
 
 struct KernelArgs {
   const void* logits;        // [B][row_stride] f32 or bf16, device
@@ -142,6 +150,11 @@ struct KernelArgs {
   uint32_t* hist_end;        // [B] end of row b's counts (hist_off[b] = kHistBad on overflow)
   uint32_t ring_cap;
   uint32_t pad2;
+  // Anti-restate rows: candidates to guard[B][kGuardWords] (device) and, in
+  // synchronous calls, to guard_mapped (mapped pinned host memory) before
+  // the row is counted in done_mapped.
+  uint32_t* guard;
+  uint32_t* guard_mapped;
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };

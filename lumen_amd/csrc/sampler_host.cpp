@@ -137,6 +137,9 @@ struct lumen_sampler {
   DevBuf cand;  // [B][kCandCap] candidate buffers
   DevBuf est;   // [B][kRowRecs][kRecWords] run records of the split top-p path
   DevBuf hist;  // [B][kMaxSlices][kMassBins] candidate mass histograms
+  DevBuf guard;  // [B][kGuardWords] anti-restate candidates when the caller passes none
+  uint32_t* guard_dev = nullptr;  // where the last call's candidates went
+  bool any_anti = false;          // the last call had anti-restate rows
   DevBuf wcnt;  // device history: [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts
   int cu_count = 0;
   int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
@@ -195,7 +198,7 @@ int ensure_dev(DevBuf& b, size_t bytes) {
 }
 
 // Resolves one row (sampling.rs:452-527). Returns LUMEN_OK or an error.
-int resolve_row(const lumen_sampling_params& p, uint32_t V, bool has_window, RowParams& r) {
+void resolve_row(const lumen_sampling_params& p, uint32_t V, bool has_window, RowParams& r) {
   std::memset(&r, 0, sizeof(r));
   r.temperature = p.temperature;
   const float rep = p.repetition_penalty, pres = p.presence_penalty, freq = p.frequency_penalty;
@@ -208,10 +211,10 @@ int resolve_row(const lumen_sampling_params& p, uint32_t V, bool has_window, Row
   r.freq = freq;
   if (pen && has_window) r.flags |= lumen::kPen;
   if (std::fabs(rep - 1.0f) >= kF32Eps) r.flags |= lumen::kRep;
-  if (p.temperature <= 0.0f) {  // greedy branch (sampling.rs:468)
-    if (p.anti_restate) return LUMEN_ERR_UNSUPPORTED;
+  if (p.temperature <= 0.0f) {  // greedy branch (sampling.rs:468-476)
     r.flags |= lumen::kGreedy;
-    return LUMEN_OK;
+    if (p.anti_restate) r.flags |= lumen::kAnti;
+    return;
   }
   if (p.top_k > 0 && p.top_k < (uint64_t)V) {  // sampling.rs:492-496
     r.flags |= lumen::kTopK;
@@ -226,7 +229,7 @@ int resolve_row(const lumen_sampling_params& p, uint32_t V, bool has_window, Row
     r.log_min_p = logf(p.min_p);
   }
   r.inv_temp = 1.0f / p.temperature;  // sampling.rs:517
-  return LUMEN_OK;
+  return;
 }
 
 // Form A: counts over the last repeat_last_n ids of the history
@@ -245,9 +248,114 @@ void count_window(lumen_sampler* s, const uint32_t* h, uint64_t len, uint64_t wi
   }
 }
 
+// ---- anti-restate rules (sampling.rs:552-836) ----
+constexpr int kAntiMaxSkip = 8;          // ANTI_RESTATE_MAX_SKIP
+constexpr size_t kLoopWindow = 28;       // ANTI_RESTATE_LOOP_WINDOW
+constexpr size_t kLoopThresh = 5;        // ANTI_RESTATE_LOOP_THRESH
+constexpr size_t kMinSuffix = 4;         // ANTI_RESTATE_MIN_SUFFIX
+constexpr size_t kMinSpan = 3, kMaxSpan = 8;  // ANTI_RESTATE_{MIN,MAX}_SPAN
+
+struct AntiRules {
+  bool subword, ngram, loop;
+};
+
+// A rule is on unless its variable reads 0 / false / no / off (sampling.rs:631-636).
+bool rule_on(const char* name) {
+  const char* e = std::getenv(name);
+  if (!e) return true;
+  return std::strcmp(e, "0") != 0 && std::strcmp(e, "false") != 0 && std::strcmp(e, "no") != 0 &&
+         std::strcmp(e, "off") != 0;
+}
+
+// Resolved once per process (sampling.rs:638-651).
+const AntiRules& anti_rules() {
+  static const AntiRules r{rule_on("LUMEN_ANTI_RESTATE_SUBWORD"), rule_on("LUMEN_ANTI_RESTATE_NGRAM"),
+                           rule_on("LUMEN_ANTI_RESTATE_LOOP")};
+  return r;
+}
+
+// u8::is_ascii_whitespace: space, \t, \n, \x0C, \r (not \x0B)
+bool ascii_ws(uint8_t c) { return c == ' ' || c == '\t' || c == '\n' || c == 0x0C || c == '\r'; }
+
+struct Bytes {
+  const uint8_t* p;
+  size_t n;
+};
+
+Bytes token_bytes(const lumen_token_bytes* d, uint32_t id) {
+  if (!d || !d->offsets || id >= d->count) return {nullptr, 0};
+  const uint64_t lo = d->offsets[id], hi = d->offsets[id + 1];
+  if (hi <= lo || !d->data) return {nullptr, 0};
+  return {d->data + lo, (size_t)(hi - lo)};
+}
+
+// sampling.rs:732-780
+bool restates_subword(uint32_t cand, const uint32_t* h, size_t hl, const lumen_token_bytes* d) {
+  if (!d || hl == 0) return false;
+  const Bytes c = token_bytes(d, cand);
+  if (c.n == 0) return false;
+  for (size_t i = 0; i < c.n; ++i)
+    if (ascii_ws(c.p[i])) return false;
+  const Bytes prev = token_bytes(d, h[hl - 1]);
+  if (prev.n == 0) return false;
+  size_t tail = 0;
+  for (size_t i = prev.n; i > 0; --i)
+    if (ascii_ws(prev.p[i - 1])) {
+      tail = i;
+      break;
+    }
+  const uint8_t* word = prev.p + tail;
+  const size_t wl = prev.n - tail;
+  if (wl < kMinSuffix) return false;
+  for (size_t sl = wl; sl >= kMinSuffix; --sl)
+    if (c.n >= sl && std::memcmp(c.p, word + (wl - sl), sl) == 0) return true;
+  return false;
+}
+
+// sampling.rs:819-836
+bool restates_ngram(uint32_t cand, const uint32_t* h, size_t hl) {
+  for (size_t k = kMinSpan; k <= kMaxSpan; ++k) {
+    if (hl + 1 < 2 * k) continue;
+    const size_t w0 = hl - (k - 1), p0 = hl - (2 * k - 1);
+    if (std::equal(h + w0, h + hl, h + p0) && cand == h[p0 + k - 1]) return true;
+  }
+  return false;
+}
+
+// sampling.rs:693-701
+bool runaway_loop(uint32_t cand, const uint32_t* h, size_t hl) {
+  if (hl < kLoopThresh) return false;
+  const size_t start = hl > kLoopWindow ? hl - kLoopWindow : 0;
+  return (size_t)std::count(h + start, h + hl, cand) >= kLoopThresh;
+}
+
+// sampling.rs:657-662
+bool degenerate(uint32_t cand, const uint32_t* h, size_t hl, const lumen_token_bytes* d) {
+  const AntiRules& r = anti_rules();
+  return (r.subword && restates_subword(cand, h, hl, d)) || (r.ngram && restates_ngram(cand, h, hl)) ||
+         (r.loop && runaway_loop(cand, h, hl));
+}
+
 }  // namespace
 
 extern "C" {
+
+uint32_t lumen_anti_restate_select(const uint32_t* cands, const uint32_t* history,
+                                   uint64_t history_len, const lumen_token_bytes* decoder) {
+  if (!cands) return LUMEN_TOKEN_ERROR;
+  const uint32_t raw = cands[0];
+  if (history_len == 0 || !history) return raw;  // sampling.rs:566-568
+  uint32_t cand = raw;
+  int j = 1;
+  for (int probe = 0; probe < kAntiMaxSkip; ++probe) {  // sampling.rs:571-583
+    if (!degenerate(cand, history, (size_t)history_len, decoder)) return cand;
+    // argmax_excluding: the next finite candidate not yet probed
+    while (j < lumen::kGuardWords && cands[j] == raw) ++j;
+    if (j >= lumen::kGuardWords || cands[j] == lumen::kGuardNone) break;
+    cand = cands[j++];
+  }
+  return raw;
+}
 
 uint64_t lumen_xorshift64_new(uint64_t seed) {
   // sampling.rs:64-83
@@ -370,16 +478,16 @@ void lumen_sampler_destroy(lumen_sampler* s) {
 
 namespace {
 int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, uint32_t* tok_map,
-                 uint32_t* done_map);
+                 uint32_t* done_map, uint32_t* guard_map, bool sync);
 }  // namespace
 
 int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream) {
-  return launch_batch(s, bt, stream, nullptr, nullptr);
+  return launch_batch(s, bt, stream, nullptr, nullptr, nullptr, false);
 }
 
 namespace {
 int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, uint32_t* tok_map,
-                 uint32_t* done_map) {
+                 uint32_t* done_map, uint32_t* guard_map, bool sync) {
   if (!s || !bt) return fail(LUMEN_ERR_INVALID, "null context or batch");
   const uint32_t B = bt->batch, V = bt->vocab;
   if (B == 0) return LUMEN_OK;
@@ -417,6 +525,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   s->cnts.clear();
   s->offs.assign(B + 1, 0);
   bool any_pen = false;
+  bool any_anti = false;
   for (uint32_t b = 0; b < B; ++b) {
     const lumen_sampling_params& p = bt->params[b];
     bool has_window = false;
@@ -431,8 +540,15 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     } else if (bt->pen_offsets) {
       has_window = true;  // an empty count range applies nothing either way
     }
-    int rc = resolve_row(p, V, has_window, rows[b]);
-    if (rc != LUMEN_OK) return fail(rc, "anti_restate is not supported on the GPU path");
+    resolve_row(p, V, has_window, rows[b]);
+    if (rows[b].flags & lumen::kAnti) {
+      any_anti = true;
+      if (sync && (bt->pen_offsets || ring))
+        return fail(LUMEN_ERR_UNSUPPORTED,
+                    "anti_restate rows need the token history (history_offsets) in a synchronous call");
+      if (!sync && !bt->guard_out)
+        return fail(LUMEN_ERR_INVALID, "anti_restate rows need guard_out in an asynchronous call");
+    }
     if (!bt->pen_offsets && !ring && (rows[b].flags & lumen::kPen))
       count_window(s, bt->history + h0, h1 - h0, p.repeat_last_n);
     s->offs[b + 1] = (uint32_t)s->ids.size();
@@ -609,6 +725,18 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   }
   ka.tokens_mapped = tok_map;
   ka.done_mapped = done_map;
+  if (any_anti) {
+    if (bt->guard_out) {
+      ka.guard = bt->guard_out;
+    } else {
+      int rc = ensure_dev(s->guard, sizeof(uint32_t) * lumen::kGuardWords * B);
+      if (rc != LUMEN_OK) return rc;
+      ka.guard = static_cast<uint32_t*>(s->guard.p);
+    }
+    ka.guard_mapped = guard_map;
+    s->guard_dev = ka.guard;
+  }
+  s->any_anti = any_anti;
   if (ring) {
     // the window counts of every row, ahead of the sampler on the same stream
     size_t hsz = sizeof(ka);
@@ -673,7 +801,9 @@ int lumen_sampler_sample_batch_sync(lumen_sampler* s, const lumen_batch* bt, uin
     s->map_dev = nullptr;
     s->map_cap = 0;
     void* h = nullptr;
-    if (hipHostMalloc(&h, sizeof(uint32_t) * (B + 1), hipHostMallocMapped | hipHostMallocCoherent) ==
+    // [0] rows written, [1 .. B] tokens, then [B][kGuardWords] guard candidates
+    if (hipHostMalloc(&h, sizeof(uint32_t) * (1 + B + (size_t)lumen::kGuardWords * B),
+                      hipHostMallocMapped | hipHostMallocCoherent) ==
         hipSuccess) {
       void* d = nullptr;
       if (hipHostGetDevicePointer(&d, h, 0) == hipSuccess) {
@@ -687,8 +817,8 @@ int lumen_sampler_sample_batch_sync(lumen_sampler* s, const lumen_batch* bt, uin
   }
   const bool mapped = s->map_host != nullptr && B > 0 && bt->vocab > 0;  // V = 0 launches nothing
   if (mapped) __atomic_store_n(&s->map_host[0], 0u, __ATOMIC_RELEASE);
-  int rc = mapped ? launch_batch(s, bt, stream, s->map_dev + 1, s->map_dev)
-                  : launch_batch(s, bt, stream, nullptr, nullptr);
+  int rc = mapped ? launch_batch(s, bt, stream, s->map_dev + 1, s->map_dev, s->map_dev + 1 + B, true)
+                  : launch_batch(s, bt, stream, nullptr, nullptr, nullptr, true);
   if (rc != LUMEN_OK) return rc;
   bool done = false;
   if (mapped) {
@@ -709,6 +839,45 @@ int lumen_sampler_sample_batch_sync(lumen_sampler* s, const lumen_batch* bt, uin
         hipSuccess)
       return LUMEN_ERR_HIP;
     if (hipStreamSynchronize(st) != hipSuccess) return LUMEN_ERR_HIP;
+  }
+  if (s->any_anti) {
+    // the guard's rules on the host (guarded_argmax, sampling.rs:563-603)
+    const uint32_t* cand = nullptr;
+    std::vector<uint32_t> cbuf;
+    if (done) {
+      cand = s->map_host + 1 + B;
+    } else {
+      cbuf.resize((size_t)lumen::kGuardWords * B);
+      if (hipMemcpyAsync(cbuf.data(), s->guard_dev, sizeof(uint32_t) * cbuf.size(),
+                         hipMemcpyDeviceToHost, st) != hipSuccess ||
+          hipStreamSynchronize(st) != hipSuccess)
+        return fail(LUMEN_ERR_HIP, "guard candidates copy");
+      cand = cbuf.data();
+    }
+    bool changed = false;
+    for (uint32_t b = 0; b < B; ++b) {
+      const lumen_sampling_params& p = bt->params[b];
+      if (!(p.temperature <= 0.0f && p.anti_restate) || tokens_host[b] == LUMEN_TOKEN_ERROR) continue;
+      const uint32_t* h = nullptr;
+      uint64_t hl = 0;
+      if (bt->history_offsets) {
+        h = bt->history + bt->history_offsets[b];
+        hl = bt->history_offsets[b + 1] - bt->history_offsets[b];
+      }
+      const uint32_t tok =
+          lumen_anti_restate_select(cand + (size_t)lumen::kGuardWords * b, h, hl, bt->decoder);
+      if (tok != tokens_host[b]) {
+        tokens_host[b] = tok;
+        changed = true;
+      }
+    }
+    if (changed) {
+      // the device copy of the tokens gets the guarded choices too
+      if (hipMemcpyAsync(bt->tokens, tokens_host, sizeof(uint32_t) * B, hipMemcpyHostToDevice, st) !=
+              hipSuccess ||
+          hipStreamSynchronize(st) != hipSuccess)
+        return fail(LUMEN_ERR_HIP, "guarded token copy");
+    }
   }
   for (uint32_t b = 0; b < bt->batch; ++b)
     if (tokens_host[b] == LUMEN_TOKEN_ERROR) return fail(LUMEN_ERR_ROW, "a row reported a failure (see its trace status)");

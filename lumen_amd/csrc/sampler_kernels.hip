@@ -1245,6 +1245,84 @@ __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const Row
   write_result(a, b, tok, tr);
 }
 
+// ---- anti-restate candidates (sampling.rs:563-603) -------------------------
+// guarded_argmax probes the raw argmax, then argmax_excluding over the finite
+// values: at most 8 probes, so the raw argmax and the 8 largest finite keys
+// ((total_cmp key << 32) | ~id: value desc, id asc) decide every outcome.
+struct Top8 {
+  uint64_t t[8];  // descending; 0 = empty (no real key is 0: ids are < 2^32 - 1)
+};
+
+__device__ __forceinline__ void top8_init(Top8& x) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) x.t[q] = 0ull;
+}
+
+__device__ __forceinline__ void top8_push(Top8& x, uint64_t k) {
+  if (k <= x.t[7]) return;
+#pragma unroll
+  for (int q = 7; q > 0; --q) x.t[q] = k > x.t[q - 1] ? x.t[q - 1] : (k > x.t[q] ? k : x.t[q]);
+  x.t[0] = k > x.t[0] ? k : x.t[0];
+}
+
+// The wave's 8 largest keys (the same in every lane) from per-lane sorted
+// lists: 8 rounds of a wave maximum over the heads, the owner popping its head.
+__device__ __forceinline__ void wave_top8(Top8& x, uint64_t out[8]) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const uint64_t m = wave_reduce(x.t[0], (uint64_t)0, op_max_u64);
+    out[r] = m;
+    if (m != 0ull && x.t[0] == m) {
+#pragma unroll
+      for (int q = 0; q < 7; ++q) x.t[q] = x.t[q + 1];
+      x.t[7] = 0ull;
+    }
+  }
+}
+
+// The block's 8 largest keys, returned in LDS (s.Bk[128 .. 135]). Uses
+// s.Bk[0 .. 135]; starts with a barrier, so s.Bk may be in use before.
+__device__ __forceinline__ const uint64_t* block_top8(Top8& x, Smem& s) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  uint64_t out[8];
+  wave_top8(x, out);
+  __syncthreads();
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) s.Bk[w * 8u + (uint32_t)r] = out[r];
+  }
+  __syncthreads();
+  if (t < 64u) {
+    Top8 y;
+    top8_init(y);
+    static_assert(kWaves * 8 <= 128, "two entries per lane");
+    top8_push(y, s.Bk[2u * lane]);
+    top8_push(y, s.Bk[2u * lane + 1u]);
+    wave_top8(y, out);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) s.Bk[128 + r] = out[r];
+    }
+  }
+  __syncthreads();
+  return s.Bk + 128;
+}
+
+__device__ __forceinline__ void write_guard(const KernelArgs& a, int b, uint32_t raw,
+                                            const uint64_t* top) {
+  if (threadIdx.x != 0) return;
+  uint32_t g[kGuardWords];
+  g[0] = raw;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) g[1 + r] = top[r] ? ~(uint32_t)top[r] : kGuardNone;
+  if (a.guard)
+#pragma unroll
+    for (int r = 0; r < kGuardWords; ++r) a.guard[(uint64_t)b * kGuardWords + r] = g[r];
+  if (a.guard_mapped)
+#pragma unroll
+    for (int r = 0; r < kGuardWords; ++r) a.guard_mapped[(uint64_t)b * kGuardWords + r] = g[r];
+}
+
 // The whole sampler for row b, run by one workgroup (used directly when a
 // row has one workgroup, and as the fallback of the split paths).
 __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b, Smem& s) {
@@ -1280,11 +1358,24 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   // ---- greedy (sampling.rs:468-476) ----
   if (P.flags & kGreedy) {
     uint64_t best = 0;
-    row_foreach(row, [&](uint32_t i, float v) {
-      uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
-      best = k > best ? k : best;
-    });
-    best = block_max_u64(best, s);
+    if (P.flags & kAnti) {
+      // the guard's candidates (sampling.rs:563-603)
+      Top8 x;
+      top8_init(x);
+      row_foreach(row, [&](uint32_t i, float v) {
+        const uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+        best = k > best ? k : best;
+        if (is_finite(v)) top8_push(x, k);
+      });
+      best = block_max_u64(best, s);
+      write_guard(a, b, 0xffffffffu - (uint32_t)best, block_top8(x, s));
+    } else {
+      row_foreach(row, [&](uint32_t i, float v) {
+        uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+        best = k > best ? k : best;
+      });
+      best = block_max_u64(best, s);
+    }
     tr.path |= 1u;
     tr.passes++;
     write_result(a, b, 0xffffffffu - (uint32_t)best, tr);
@@ -1799,6 +1890,79 @@ __device__ __forceinline__ void slice_pen_out(const KernelArgs& a, int b, const 
   const Row row = make_row((a), (b));                                                 \
   (void)rdraw;                                                                        \
   (void)cand
+
+// Greedy with the anti-restate guard, split over G workgroups: the argmax as
+// in greedy_split, and each slice's 8 largest finite penalized keys; the
+// finisher merges them.
+__device__ __forceinline__ void greedy_guard_split(const KernelArgs& a, int b, uint32_t sl,
+                                                   uint32_t G, Smem& s) {
+  ROW_CONTEXT(a, b);
+  const uint32_t V = a.vocab;
+  const Slice sc = slice_bounds(V, G, sl);
+  const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
+  if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
+  const uint32_t* bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
+  uint64_t best = 0;
+  Top8 x;
+  top8_init(x);
+  range_foreach(row, sc.lo, sc.hi, [&](uint32_t i, float v) {
+    if (pen && bm_test(bm, i - sc.lo)) return;
+    const uint64_t k = ((uint64_t)tkey(v) << 32) | (uint64_t)(0xffffffffu - i);
+    best = k > best ? k : best;
+    if (is_finite(v)) top8_push(x, k);
+  });
+  if (pen) {
+    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
+    for (uint32_t j = h0 + threadIdx.x; j < h1; j += kThreads) {
+      const uint32_t id = a.hist_ids[j];
+      if (id >= sc.lo && id < sc.hi) {
+        const float pv = penalize(row.at(id), a.hist_cnt[j], P);
+        const uint64_t k = ((uint64_t)tkey(pv) << 32) | (uint64_t)(0xffffffffu - id);
+        best = k > best ? k : best;
+        if (is_finite(pv)) top8_push(x, k);
+      }
+    }
+  }
+  best = block_max_u64(best, s);
+  const uint64_t* top = block_top8(x, s);
+  if (threadIdx.x == 0) {
+    ws.part_arg[sl] = best;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ws.part_top[sl][r] = top[r];
+  }
+  const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
+  if (old != G - 1u) return;
+  if (threadIdx.x < 64u) {
+    const uint32_t lane = threadIdx.x;
+    uint64_t m = 0;
+    for (uint32_t i = 0; i < G; ++i) {
+      const uint64_t u = __hip_atomic_load(&ws.part_arg[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      m = u > m ? u : m;
+    }
+    Top8 y;
+    top8_init(y);
+    uint64_t* pt = &ws.part_top[0][0];
+#pragma unroll
+    for (uint32_t q = 0; q < 2u; ++q)
+      if (2u * lane + q < G * 8u)
+        top8_push(y, __hip_atomic_load(&pt[2u * lane + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    uint64_t out[8];
+    wave_top8(y, out);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) s.Bk[r] = out[r];
+      s.Bk[8] = m;
+    }
+  }
+  __syncthreads();
+  const uint64_t m = s.Bk[8];
+  write_guard(a, b, 0xffffffffu - (uint32_t)m, s.Bk);
+  RowTrace tr;
+  init_trace(tr, V);
+  tr.path = 1u;
+  tr.passes = 1;
+  write_result(a, b, 0xffffffffu - (uint32_t)m, tr);
+}
 
 // Greedy: per-slice argmax, the last workgroup to arrive combines.
 __device__ __forceinline__ void greedy_split(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
@@ -2758,7 +2922,10 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
     const uint64_t top_k = P.top_k;
     const uint32_t per = ((a.vocab + G - 1u) / G + 15u) & ~15u;
     if (flags & kGreedy) {
-      greedy_split(a, (int)b, sl, G, s);
+      if (flags & kAnti)
+        greedy_guard_split(a, (int)b, sl, G, s);
+      else
+        greedy_split(a, (int)b, sl, G, s);
     } else if ((flags & kTopK) && top_k <= 2048u) {
       topk_split(a, (int)b, sl, G, s);
     } else if ((flags & kTopP) && !(flags & (kTopK | kPen)) &&

@@ -155,7 +155,7 @@ class Engine:
                      rngs: Optional[Sequence[Xorshift64]] = None,
                      penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
                      sync: bool = True, stream=None, uniforms_dev=None, rng_states_dev=None,
-                     hist_ring_dev=None, hist_len_dev=None):
+                     hist_ring_dev=None, hist_len_dev=None, guard_out=None, decoder=None):
         """Samples every row of `logits` [B, V].
 
         histories: SamplerState.history per row (the window is applied here),
@@ -168,6 +168,10 @@ class Engine:
         hist_ring_dev / hist_len_dev: device-resident history (an int32
         [B, cap] ring and an int32 [B] count of recorded tokens); the window
         is counted on the device and each row's token recorded there.
+        guard_out: an int32 device [B, 9] tensor for the anti-restate
+        candidates (required for anti_restate rows when sync=False);
+        decoder: TokenBytes (or a list of bytes per id) for the guard's
+        sub-word rule.
         Returns the token tensor (device); with sync=True also a host list.
         """
         import torch
@@ -211,6 +215,13 @@ class Engine:
             bt.hist_ring_dev = hist_ring_dev.data_ptr()
             bt.hist_len_dev = hist_len_dev.data_ptr()
             bt.hist_cap = hist_ring_dev.shape[1]
+        if guard_out is not None:
+            bt.guard_out = guard_out.data_ptr()
+        if decoder is not None:
+            if not isinstance(decoder, TokenBytes):
+                decoder = TokenBytes(decoder)
+            keep.append(decoder)
+            bt.decoder = ctypes.pointer(decoder.c)
         if uniforms_dev is not None:
             bt.uniforms_dev = uniforms_dev.data_ptr()
         elif rng_states_dev is not None:
@@ -247,6 +258,34 @@ class Engine:
                 r.set_state(int(v))
         _native.check(rc, "lumen_sampler_sample_batch")
         return (tokens_out, list(host)) if sync else (tokens_out, None)
+
+
+class TokenBytes:
+    """The embedder's per-id byte decoder (SamplerState::decoder,
+    sampling.rs:343-378) as a table: table[i] is the bytes of id i."""
+
+    def __init__(self, table: Sequence[bytes]):
+        blobs = [bytes(b) for b in table]
+        self.offsets = np.zeros(len(blobs) + 1, dtype=np.uint64)
+        self.offsets[1:] = np.cumsum([len(b) for b in blobs])
+        self.data = np.frombuffer(b"".join(blobs) + b"\0", dtype=np.uint8).copy()
+        self.c = _native.TokenBytesC(self.data.ctypes.data, self.offsets.ctypes.data, len(blobs))
+
+
+def anti_restate_select(candidates: Sequence[int], history: Sequence[int],
+                        decoder=None) -> int:
+    """guarded_argmax (sampling.rs:563-603) from the 9 device candidates of
+    a row (guard_out[b]) and its history, through the library."""
+    L = _native.load()
+    c = (ctypes.c_uint32 * 9)(*[int(x) & 0xFFFFFFFF for x in candidates])
+    h = np.ascontiguousarray(np.asarray(history, dtype=np.uint32).reshape(-1))
+    d = None
+    if decoder is not None:
+        if not isinstance(decoder, TokenBytes):
+            decoder = TokenBytes(decoder)
+        d = ctypes.pointer(decoder.c)
+    return int(L.lumen_anti_restate_select(
+        c, h.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), h.size, d))
 
 
 class DeviceDecodeState:

@@ -445,3 +445,62 @@ def test_device_history_overflow(eng):
     assert list(lens) == [20, 21, 21]
     with pytest.raises(RuntimeError):
         ds.step(eng, lg, params)
+
+
+@pytest.mark.parametrize("V", [3000, 248320])
+def test_anti_restate_guard(eng, V):
+    # Greedy rows with anti_restate (sampling.rs:472-474): the device picks the
+    # guard's candidates from the (penalized) row, the host applies the rules.
+    # Tokens against the oracle's sample_logits with the same history and
+    # decoder; candidates against numpy's top finite keys.
+    import torch
+    from lumen_amd.sampling import TokenBytes
+    from oracle import oracle as o
+    from tests.test_anti_restate_cpu import candidates
+
+    rng = np.random.default_rng(V + 1)
+    B = 16
+    alpha = [b"ab", b"ba", b"abab", b" ab", b"b", b"cab"]
+    table = [alpha[int(i)] * int(rng.integers(1, 3)) for i in rng.integers(0, len(alpha), V)]
+    dec = TokenBytes(table)
+    lg = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    params, hists = [], []
+    for b in range(B):
+        loop = rng.integers(0, V, size=int(rng.integers(1, 5))).astype(np.uint32)
+        h = np.resize(loop, int(rng.integers(0, 30))).astype(np.uint32)
+        # make the restating / looping tokens the leaders
+        for j, tok in enumerate(np.unique(h)[:6]):
+            lg[b, tok] = 9.0 - 0.25 * j
+        if b % 4 == 3:
+            lg[b, int(rng.integers(0, V))] = np.nan
+        if b % 5 == 4:
+            lg[b, rng.integers(0, V, size=3)] = np.inf
+        pen = {} if b % 2 else dict(repetition_penalty=1.3, repeat_last_n=8)
+        params.append(SP(temperature=0.0, anti_restate=True, **pen))
+        hists.append(h)
+    x = torch.from_numpy(lg).to("cuda:0")
+    log(f"case anti_restate V={V} sync")
+    _, got = eng.sample_batch(x, params, histories=hists, decoder=dec)
+    want = []
+    for b in range(B):
+        op = o.Params(temperature=0.0, anti_restate=True,
+                      repetition_penalty=params[b].repetition_penalty,
+                      repeat_last_n=params[b].repeat_last_n)
+        want.append(o.sample_logits(lg[b].copy(), op, hists[b], o.Xorshift64(1), table))
+    assert got == want
+    # asynchronous: raw argmax in tokens, candidates in guard_out
+    log(f"case anti_restate V={V} async")
+    gout = torch.full((B, 9), -7, dtype=torch.int32, device="cuda:0")
+    toks, _ = eng.sample_batch(x, params, histories=hists, guard_out=gout, sync=False)
+    torch.cuda.synchronize()
+    g = gout.cpu().numpy().view(np.uint32)
+    t = toks.cpu().numpy().view(np.uint32)
+    for b in range(B):
+        if params[b].repetition_penalty is None:
+            assert list(g[b]) == candidates(lg[b]), b
+        assert t[b] == g[b][0]
+    # the sync tokens are the guard's choice over those candidates
+    from lumen_amd.sampling import anti_restate_select
+    assert [anti_restate_select(g[b], hists[b], dec) for b in range(B)] == want
+    with pytest.raises(Exception):
+        eng.sample_batch(x, params, histories=hists, sync=False)

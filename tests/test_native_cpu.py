@@ -17,7 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_functions():
     src = open(os.path.join(ROOT, "include", "lumen_sampler.h")).read()
-    return sorted(set(re.findall(r"^\s*(?:int|void|float|uint64_t|const char \*)\s*\*?\s*"
+    return sorted(set(re.findall(r"^\s*(?:int|void|float|uint64_t|uint32_t|const char \*)\s*\*?\s*"
                                  r"(lumen_\w+)\s*\(", src, re.M)))
 
 
@@ -100,7 +100,33 @@ def test_struct_layouts():
     # lumen_sampling_params: 6 floats, 2 u64, 2 i32 = 48 bytes
     assert ctypes.sizeof(_native.SamplingParamsC) == 48
     assert ctypes.sizeof(_native.RowTraceC) == 64
-    assert ctypes.sizeof(_native.BatchC) == 160
+    assert ctypes.sizeof(_native.BatchC) == 176
+    assert ctypes.sizeof(_native.TokenBytesC) == 24
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    # every field offset of the ctypes mirrors equals the C compiler's
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    structs = {"lumen_batch": _native.BatchC, "lumen_sampling_params": _native.SamplingParamsC,
+               "lumen_row_trace": _native.RowTraceC, "lumen_token_bytes": _native.TokenBytesC}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "lumen_sampler.h"',
+             "int main(void) {"]
+    want = []
+    for cname, py in structs.items():
+        lines.append(f'printf("%zu\\n", sizeof({cname}));')
+        want.append(ctypes.sizeof(py))
+        for f in py._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({cname}, {f[0]}));')
+            want.append(getattr(py, f[0]).offset)
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(root, "include"), "-o", str(exe), str(src)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    assert got == want
 
 
 def test_create_without_gpu_fails_cleanly():
