@@ -21,6 +21,8 @@ The JSON line also carries:
                 this host, single thread, over the same 64 rows
   b1_latency    config 2 (B=1, V=248,320): p50/p99 wall time per draw of
                 sequential draws (launch + 4-byte readback + sync)
+  b1_decode_device_state  the same as a decode loop with the RNG state and
+                the history on the device (no host draw, no history upload)
 """
 import argparse
 import json
@@ -163,6 +165,31 @@ def b1_latency(eng, draws=10_000):
     return float(np.percentile(times, 50)), float(np.percentile(times, 99)), len(times)
 
 
+def b1_decode_device_state(eng, draws=2_000):
+    """Config 2 as a decode loop with the state on the device: the history
+    ring (whole-history penalty window, counted on the device each draw) and
+    the Xorshift64 state live in HBM; per draw one call (the window-count
+    kernel and the sampler) and a 4-byte readback."""
+    import torch
+
+    from lumen_amd.sampling import DeviceDecodeState
+    from lumen_amd.workloads import config2
+
+    w = config2()
+    dev = torch.from_numpy(w.logits).cuda()
+    ds = DeviceDecodeState(w.seeds, cap=8192, histories=w.histories)
+    tok = torch.empty(1, dtype=torch.int32, device=dev.device)
+    times = []
+    for i in range(draws + 50):
+        t0 = time.perf_counter()
+        ds.step(eng, dev, w.params, tokens_out=tok, sync=True)
+        t1 = time.perf_counter()
+        if i >= 50:
+            times.append((t1 - t0) * 1e6)
+    times = np.array(times)
+    return float(np.percentile(times, 50)), float(np.percentile(times, 99)), len(times)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -258,6 +285,11 @@ def main():
         line["b1_latency"] = {"p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
                               "workload": "config2: B=1 V=248320 f32, top_k 20 top_p 0.8 "
                                           "presence 1.5 frequency 0.5"}
+        p50, p99, n = b1_decode_device_state(eng)
+        line["b1_decode_device_state"] = {
+            "p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
+            "workload": "config2 decode loop: RNG state and a 8192-token history ring on "
+                        "the device, whole-history penalty window counted per draw"}
     if not args.no_cpu:
         rate, rows, reps, cel = cpu_baseline(w, u_host)
         line["cpu_baseline"] = {"value": round(rate, 2), "unit": "samples/s", "cores": 1,
