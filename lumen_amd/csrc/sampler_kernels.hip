@@ -1323,6 +1323,319 @@ __device__ __forceinline__ void write_guard(const KernelArgs& a, int b, uint32_t
     for (int r = 0; r < kGuardWords; ++r) a.guard_mapped[(uint64_t)b * kGuardWords + r] = g[r];
 }
 
+// ---- top-p over distinct values (bf16 rows) ---------------------------------
+// A bf16 row holds at most 65536 distinct values, and equal values have equal
+// probabilities, so the cumulative sum of apply_top_p_on_logits
+// (sampling.rs:942-967) in (p desc, id asc) order is a walk over the distinct
+// values in descending order, each value's p added once per occurrence.
+// Adding one summand p c times inside a binade of the running sum is closed
+// form on the grid (the facts of ecss.h): with p = (q + f) grid steps, every
+// add moves q steps (f < 1/2) or q + 1 (f > 1/2); for f = 1/2 the first add
+// rounds to the even neighbour and every later one moves by the even of
+// q and q + 1. So a distinct value is one parity map, and the walk is the
+// one-wave parity-map scan of wave_ecss with values in place of elements.
+
+// occurrences of the value whose total_cmp key has the upper half pk, from u16 counts
+__device__ __forceinline__ uint32_t vcount(const uint32_t* cw, uint32_t pk) {
+  return (cw[pk >> 1] >> ((pk & 1u) << 4)) & 0xffffu;
+}
+
+// Increment map (grid steps, by incoming parity) of adding p c times inside
+// the binade with exponent field E; {kSat, kSat} when one add may leave it.
+__device__ __forceinline__ PMap rep_map(float p, uint32_t c, uint32_t E) {
+  if (c == 0u) return PMap{0u, 0u};
+  const double pu = ldexp((double)p, 150 - (int)(E ? E : 1u));
+  if (!(pu < 16777216.0)) return PMap{kSat, kSat};
+  const uint64_t q = (uint64_t)pu;
+  const double f = pu - (double)q;
+  uint64_t a0, a1;
+  if (f < 0.5) {
+    a0 = a1 = (uint64_t)c * q;
+  } else if (f > 0.5) {
+    a0 = a1 = (uint64_t)c * (q + 1u);
+  } else if (!(q & 1u)) {
+    a0 = (uint64_t)c * q;
+    a1 = a0 + 1u;
+  } else {
+    a0 = (uint64_t)c * (q + 1u);
+    a1 = a0 - 1u;
+  }
+  return PMap{(uint32_t)(a0 > kSat ? kSat : a0), (uint32_t)(a1 > kSat ? kSat : a1)};
+}
+
+// c adds of p to y in sequence from y's exact value: closed form inside each
+// binade, one real add for each add that changes binade. With `find`, stops
+// at the first add whose result is >= theta: returns true, j = its 0-based
+// index, prev = the sum before it.
+__device__ __forceinline__ bool rep_replay(float& y, float& prev, float p, uint32_t c, float theta,
+                                           bool find, uint32_t& j) {
+  uint32_t done = 0;
+  prev = y;
+  while (done < c) {
+    const uint32_t cb = __float_as_uint(y);
+    const uint32_t E = cb >> 23;
+    const uint32_t ub = (cb & 0xff800000u) + 0x00800000u;
+    const double pu = ldexp((double)p, 150 - (int)(E ? E : 1u));
+    uint32_t i0 = 0, d = 0;
+    bool real = !(pu < 16777216.0);
+    if (!real) {
+      const uint32_t q = (uint32_t)pu;
+      const double f = pu - (double)q;
+      if (f < 0.5) {
+        i0 = d = q;
+      } else if (f > 0.5) {
+        i0 = d = q + 1u;
+      } else {
+        i0 = (((cb & 1u) + q) & 1u) ? q + 1u : q;
+        d = q + (q & 1u);
+      }
+      if (i0 > ub - 1u - cb) real = true;
+    }
+    if (real) {
+      prev = y;
+      y = __fadd_rn(y, p);
+      if (find && y >= theta) {
+        j = done;
+        return true;
+      }
+      ++done;
+      continue;
+    }
+    if (i0 == 0u && d == 0u) return false;  // no add moves y any more
+    const uint32_t room = ub - 1u - cb;
+    const uint64_t fit = d ? 1u + (uint64_t)(room - i0) / d : (uint64_t)c;
+    const uint32_t n = (uint32_t)(fit < (uint64_t)(c - done) ? fit : (uint64_t)(c - done));
+    auto val = [&](uint32_t k) { return __uint_as_float(cb + i0 + (k - 1u) * d); };  // after k adds
+    if (find && val(n) >= theta) {
+      uint32_t lo = 1u, hi = n;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (val(mid) >= theta) hi = mid; else lo = mid + 1u;
+      }
+      prev = lo > 1u ? val(lo - 1u) : y;
+      y = val(lo);
+      j = done + lo - 1u;
+      return true;
+    }
+    prev = n > 1u ? val(n - 1u) : y;
+    y = val(n);
+    done += n;
+  }
+  return false;
+}
+
+struct ValHit {
+  bool found;
+  uint32_t lane;  // lane of the value holding the crossing
+  uint32_t j;     // 0-based occurrence of that value at the crossing
+  float c;        // running sum after the crossing add (or after the chunk)
+};
+
+// One chunk of 64 distinct values (lane order = walk order), on one wave.
+// c: the running sum, updated. Uniform result.
+__device__ __forceinline__ ValHit wave_values(float& c, float p, uint32_t cnt, float theta) {
+  const int lane = threadIdx.x & 63;
+  int t0 = 0;
+  for (;;) {
+    const uint32_t cb = __float_as_uint(c);
+    const uint32_t ub = (cb & 0xff800000u) + 0x00800000u;
+    const bool act = lane >= t0;
+    const PMap m = act ? rep_map(p, cnt, cb >> 23) : PMap{0u, 0u};
+    const PMap id{0u, 0u};
+    const PMap ex = wave_shr1(wave_scan_incl(m, id, pm_combine), id);
+    const uint32_t par0 = cb & 1u;
+    const uint32_t before = par0 ? ex.a1 : ex.a0;
+    const uint32_t own = ((par0 ^ before) & 1u) ? m.a1 : m.a0;
+    const uint32_t sbits = cb + before;
+    const uint32_t ebits = sbits + own;
+    const bool cross = act && (before >= kSat || ebits >= ub);
+    const bool hit = act && !cross && cnt && __uint_as_float(ebits) >= theta;
+    const unsigned long long bm = __ballot(cross), hm = __ballot(hit);
+    const int tb = bm ? __ffsll((long long)bm) - 1 : 64;
+    const int th = hm ? __ffsll((long long)hm) - 1 : 64;
+    if (th < 64 || tb < 64) {
+      const int r = th < tb ? th : tb;
+      float y = __uint_as_float(sbits), prev = y;
+      uint32_t j = 0;
+      bool f = false;
+      if (lane == r) f = rep_replay(y, prev, p, cnt, theta, true, j);
+      const bool fr = __builtin_amdgcn_readlane((int)f, r) != 0;
+      const float yr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(y), r));
+      if (fr) {
+        c = yr;
+        return ValHit{true, (uint32_t)r, (uint32_t)__builtin_amdgcn_readlane((int)j, r), yr};
+      }
+      c = yr;
+      t0 = r + 1;
+      if (t0 < 64) continue;
+    } else {
+      c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)ebits, 63));
+    }
+    return ValHit{false, 0u, 0u, c};
+  }
+}
+
+// Counts of a bf16 row by value, taken during the top-p max pass: u16
+// counts of every bf16 value in s.A / s.Bk (by the upper half of its
+// total_cmp key), and per block of 256 values in s.H[0 .. 255].
+__device__ __forceinline__ uint32_t* bv_counts(Smem& s) { return reinterpret_cast<uint32_t*>(s.A); }
+
+__device__ __forceinline__ void bv_clear(Smem& s) {
+  static_assert(sizeof(s.A) + sizeof(s.Bk) == 65536 * 2, "u16 counts of every bf16 value");
+  uint32_t* cw = bv_counts(s);  // s.A and s.Bk are adjacent
+  for (uint32_t i = threadIdx.x; i < 32768u; i += kThreads) cw[i] = 0u;
+  for (uint32_t i = threadIdx.x; i < 256u; i += kThreads) s.H[i] = 0u;
+}
+
+__device__ __forceinline__ void bv_count(float x, Smem& s) {
+  const uint32_t pk = tkey(x) >> 16;
+  atomicAdd(&bv_counts(s)[pk >> 1], 1u << ((pk & 1u) << 4));
+  atomicAdd(&s.H[pk >> 8], 1u);
+}
+
+// The value with key upper half pk: a negative value's key carries ones in
+// its low 16 bits.
+__device__ __forceinline__ float bv_value(uint32_t pk) {
+  return key2f((pk << 16) | ((pk & 0x8000u) ? 0u : 0xffffu));
+}
+
+// Top-p of a bf16 row by distinct value, after bv_count over every element
+// (x = vf(i, v), bf16-exact). m1 / S1: the row max and softmax sum at T = 1.
+// Returns -1 when a value may occur 65536 times or more (the caller takes
+// the window path), 0 when the cumulative sum never reaches top_p (every
+// token kept), else 1 with the kept set
+//   {x : key(x) >> 16 > pk_hi} + {x : pk_lo <= key(x) >> 16 <= pk_hi, id <= istar},
+// [pk_lo, pk_hi] being the values whose p equals the crossing's. Sets the
+// top-p trace fields. Uses s.A, s.Bk and s.H.
+template <class VF>
+__device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, float m1, float S1,
+                                                       float top_p, Smem& s, RowTrace& tr,
+                                                       uint32_t& pk_lo, uint32_t& pk_hi,
+                                                       uint32_t& istar) {
+  const uint32_t t = threadIdx.x, V = row.V;
+  const uint32_t* cw = bv_counts(s);
+  // a block of 256 values under 65536 occurrences bounds every u16 count
+  if (V > (1u << 22) || block_or_u32(t < 256u && s.H[t] > 0xffffu ? 1u : 0u, s)) return -1;
+  auto pof = [&](uint32_t pk) { return __fdiv_rn(expf_glibc(__fsub_rn(bv_value(pk), m1)), S1); };
+  if (t < 64u) {
+    const uint32_t lane = t;
+    float c = 0.f;
+    uint32_t rank = 0, pks = 0;
+    ValHit h{false, 0u, 0u, 0.f};
+    float ph = 0.f;
+    for (int blk = 255; blk >= 0 && !h.found; --blk) {
+      if (s.H[blk] == 0u) continue;
+      for (int sub = 3; sub >= 0; --sub) {
+        const uint32_t pk = (uint32_t)blk * 256u + (uint32_t)sub * 64u + (63u - lane);
+        const uint32_t cnt = vcount(cw, pk);
+        if (__ballot(cnt != 0u) == 0ull) continue;
+        const float p = cnt ? pof(pk) : 0.f;
+        h = wave_values(c, p, cnt, top_p);
+        if (h.found) {
+          rank += wave_reduce(lane < h.lane ? cnt : 0u, 0u, op_add_u32) + h.j + 1u;
+          ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), (int)h.lane));
+          pks = (uint32_t)__builtin_amdgcn_readlane((int)pk, (int)h.lane);
+          break;
+        }
+        rank += wave_reduce(cnt, 0u, op_add_u32);
+      }
+    }
+    // the values around the crossing's with the same p (p is monotone in
+    // the value, so they are adjacent among the values present)
+    uint32_t hi = pks, lo = pks;
+    if (h.found) {
+      for (uint32_t base = pks + 1u; base <= 0xffffu; base += 64u) {
+        const uint32_t pk = base + lane;
+        const uint32_t cnt = pk <= 0xffffu ? vcount(cw, pk) : 0u;
+        const bool other = cnt && pof(pk) != ph;
+        const unsigned long long om = __ballot(other);
+        const unsigned long long em = __ballot(cnt && !other) &
+                                      (om ? ((1ull << (__ffsll((long long)om) - 1)) - 1ull) : ~0ull);
+        if (em) hi = base + 63u - (uint32_t)__clzll((long long)em);
+        if (om) break;
+      }
+      for (int base = (int)pks - 1; base >= 0; base -= 64) {
+        const int pk = base - (int)lane;
+        const uint32_t cnt = pk >= 0 ? vcount(cw, (uint32_t)pk) : 0u;
+        const bool other = cnt && pof((uint32_t)pk) != ph;
+        const unsigned long long om = __ballot(other);
+        const unsigned long long em = __ballot(cnt && !other) &
+                                      (om ? ((1ull << (__ffsll((long long)om) - 1)) - 1ull) : ~0ull);
+        if (em) lo = (uint32_t)(base - (63 - __clzll((long long)em)));
+        if (om) break;
+      }
+    }
+    if (lane == 0) {
+      s.misc_u[0] = h.found ? 1u : 0u;
+      s.misc_u[1] = rank;
+      s.misc_u[2] = lo;
+      s.misc_u[3] = hi;
+      s.red_f[0] = c;
+    }
+  }
+  __syncthreads();
+  const bool found = s.misc_u[0] != 0u;
+  const uint32_t rank = s.misc_u[1];
+  pk_lo = s.misc_u[2];
+  pk_hi = s.misc_u[3];
+  tr.topp_cum = s.red_f[0];
+  __syncthreads();
+  LUMEN_TICK("bv_walk", 0);
+  if (!found) {
+    tr.topp_kept = V;
+    return 0;
+  }
+  tr.topp_kept = rank;
+  // tokens with a larger p: the counts of the values above pk_hi
+  uint32_t gt = 0;
+  for (uint32_t pk = pk_hi + 1u + t; pk <= 0xffffu; pk += kThreads) gt += vcount(cw, pk);
+  gt = block_sum_u32(gt, s);
+  // the kept set ends at the (rank - gt)-th id, in id order, of the tokens
+  // valued in [pk_lo, pk_hi]: an id histogram (lowest ids at the top) finds
+  // its bin, then a bitmap of that bin its id
+  const uint32_t k = rank - gt;
+  uint32_t sh = 0;
+  while ((V - 1u) >> sh >= 2048u) ++sh;  // bins of at most 2048 ids (V <= 2^22)
+  clear_hist(s.H, 2048);
+  __syncthreads();
+  row_foreach(row, [&](uint32_t i, float v) {
+    const uint32_t pk = tkey(vf(i, v)) >> 16;
+    if (pk >= pk_lo && pk <= pk_hi) atomicAdd(&s.H[2047u - (i >> sh)], 1u);
+  });
+  tr.passes++;
+  uint32_t ab = 0;
+  const int d = find_from_top(s.H, 2048, k, &ab, s);
+  const uint32_t lo = (2047u - (uint32_t)d) << sh, hi = min(V, lo + (1u << sh));
+  const uint32_t kk = k - ab;
+  uint32_t* bits = s.H + 2048;  // one bit per id of the bin
+  for (uint32_t i = t; i < 64u; i += kThreads) bits[i] = 0u;
+  __syncthreads();
+  range_foreach(row, lo, hi, [&](uint32_t i, float v) {
+    const uint32_t pk = tkey(vf(i, v)) >> 16;
+    if (pk >= pk_lo && pk <= pk_hi) atomicOr(&bits[(i - lo) >> 5], 1u << ((i - lo) & 31u));
+  });
+  __syncthreads();
+  if (t == 0) {
+    uint32_t left = kk, id = lo;
+    for (uint32_t w = 0; w < 64u; ++w) {
+      const uint32_t n = __popc(bits[w]);
+      if (left <= n) {
+        uint32_t m = bits[w];
+        for (uint32_t q = 1; q < left; ++q) m &= m - 1u;
+        id = lo + w * 32u + (uint32_t)(__ffs(m) - 1);
+        break;
+      }
+      left -= n;
+    }
+    s.misc_u[2] = id;
+  }
+  __syncthreads();
+  istar = s.misc_u[2];
+  __syncthreads();
+  LUMEN_TICK("bv_istar", 0);
+  return 1;
+}
+
 // The whole sampler for row b, run by one workgroup (used directly when a
 // row has one workgroup, and as the fallback of the split paths).
 __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b, Smem& s) {
@@ -1331,6 +1644,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   const uint32_t V = a.vocab;
   RowTrace tr;
   init_trace(tr, V);
+  LUMEN_TICK("rs_start", b);
 
   Row row = make_row(a, b);
 
@@ -1468,10 +1782,12 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   // value after the top-k mask (large path)
   auto v1f = [&](float v) -> float { return (kmask && tkey(v) < kcut) ? kNegInf : v; };
 
-  int pmode = 0;        // 0 none, 1 uniform index prefix, 2 probability threshold
+  int pmode = 0;        // 0 none, 1 uniform index prefix, 2 probability threshold, 3 value threshold
   uint32_t plim = 0;    // pmode 1: keep idx <= plim
   float m1 = 0.f, S1 = 1.f, pstar = 0.f;
   uint32_t istar = 0;   // pmode 2: keep p > pstar or (p == pstar and idx <= istar)
+  uint32_t pk_lo = 0, pk_hi = 0;  // pmode 3 (bf16 by value): keep value > pk_hi, or in
+                                  // [pk_lo, pk_hi] with idx <= istar (keys' upper halves)
 
   if (!small) tr.path |= 4u;
 
@@ -1479,14 +1795,22 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   if ((P.flags & kTopP) && !small) {
     float m = kNegInf;
     uint32_t nan = 0;
+    // bf16 rows also count their values (top-p by distinct value)
+    const bool bf = !row.f;
+    if (bf) {
+      bv_clear(s);
+      __syncthreads();
+    }
     row_foreach(row, [&](uint32_t i, float v) {
       float x = v1f(v);
       m = rmax(m, x);
       nan |= is_nan(x) ? 1u : 0u;
+      if (bf) bv_count(x, s);
     });
     m = block_rmax(m, s);
     nan = block_or_u32(nan, s);
     tr.passes++;
+    LUMEN_TICK("rs_topp_max", b);
     m1 = m;
     topp_done = true;
     if (!is_finite(m1)) {
@@ -1521,13 +1845,25 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       tr.passes++;
       S1 = e.c;
       tr.topp_sum = S1;
-      // walk the probability order window by window
+      LUMEN_TICK("rs_S1", b);
+      float c = 0.f;
+      bool found = false;
+      // bf16 rows: the walk over distinct values
+      const int byval = !bf ? -1
+                            : topp_by_value(row, [&](uint32_t, float v) { return v1f(v); }, m1, S1,
+                                            P.top_p, s, tr, pk_lo, pk_hi, istar);
+      LUMEN_TICK("rs_byval", b);
+      if (byval >= 0) {
+        tr.windows = 1;
+        c = tr.topp_cum;
+        found = byval == 1;
+        if (found) pmode = 3;
+      }
+      // otherwise walk the probability order window by window
       uint64_t key_hi = 1ull << 32;
       float p_hi = __uint_as_float(0x7f800000u);
-      float c = 0.f;
       uint32_t ranks = 0;
-      bool found = false;
-      for (;;) {
+      for (; byval < 0;) {
         // plan the next window [L, key_hi) of at most kCapWindow keys
         uint32_t L = 0;
         bool empty = false, overflow = false;
@@ -1666,6 +2002,9 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
     } else if (pmode == 2) {
       float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
       if (!(p > pstar || (p == pstar && i <= istar))) x = kNegInf;
+    } else if (pmode == 3) {
+      const uint32_t pk = tkey(x) >> 16;
+      if (!(pk > pk_hi || (pk >= pk_lo && i <= istar))) x = kNegInf;
     }
     return x;
   };
@@ -1676,6 +2015,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
     row_foreach(row, [&](uint32_t i, float v) { m = rmax(m, v2f(i, v)); });
     m = block_rmax(m, s);
     tr.passes++;
+    LUMEN_TICK("rs_minp_max", b);
     if (is_finite(m)) {
       mmask = true;
       bound = __fadd_rn(m, P.log_min_p);
@@ -1696,6 +2036,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   m3 = block_rmax(m3, s);
   nan3 = block_or_u32(nan3, s);
   tr.passes++;
+  LUMEN_TICK("rs_m3", b);
   tr.final_max = m3;
   uint32_t tok;
   if (!is_finite(m3)) {
@@ -1715,6 +2056,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
         row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, kEcssSum,
         0.f, s);
     tr.passes++;
+    LUMEN_TICK("rs_S3", b);
     const float S3 = S.c;
     tr.final_sum = S3;
     EcssResult e = row_ecss(
@@ -1722,6 +2064,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
         [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
         kEcssFindGt, rdraw, s);
     tr.passes++;
+    LUMEN_TICK("rs_cdf", b);
     tr.cdf_before = e.found ? e.before : e.c;
     tr.cdf_at = e.c;
     tok = e.found ? (uint32_t)e.pos : V - 1;

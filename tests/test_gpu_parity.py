@@ -241,6 +241,38 @@ def test_bf16_rows(eng):
     assert_clean(rep, "bf16")
 
 
+def test_bf16_topp_by_value(eng):
+    # bf16 rows take the top-p walk over distinct values (one workgroup per
+    # row): flat rows with large nuclei, heavy exact ties, distinct values
+    # whose probabilities round equal (tiny p), a top-k mask in front
+    # (top_k > 2048), min-p and temperature after, and crossings at
+    # low and high top_p
+    from lumen_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(17)
+    V = 40_000
+    rows, params = [], []
+    for top_p in (0.3, 0.9, 0.99, 0.9999):
+        rows.append(rng.normal(0, 1, V))
+        params.append(SP(temperature=1.0, top_p=top_p))
+    rows.append(rng.integers(-4, 5, V) * 0.5)                     # 17 distinct values
+    params.append(SP(temperature=0.7, top_p=0.95))
+    rows.append(rng.normal(0, 1, V) - 60.0 * (rng.random(V) < 0.5))  # a tail of tiny p
+    params.append(SP(temperature=1.0, top_p=0.999999))
+    rows.append(rng.normal(0, 2, V))
+    params.append(SP(temperature=1.3, top_p=0.97, top_k=5000, min_p=0.001))
+    rows.append(np.full(V, 1.5))                                  # one value everywhere
+    params.append(SP(temperature=1.0, top_p=0.5))
+    bits = to_bf16_bits(np.array(rows, dtype=np.float32))
+    f32 = (bits.astype(np.uint32) << 16).view(np.float32)
+    B = len(rows)
+    for rep_i, u in enumerate((rng.random(B), np.full(B, 0.999), np.zeros(B))):
+        log(f"case bf16 by value {rep_i}")
+        rep = parity.compare(eng, f32, params, [np.zeros(0, np.uint32)] * B,
+                             u.astype(np.float32), dtype="bf16", bf16_bits=bits)
+        assert_clean(rep, f"bf16 by value {rep_i}")
+
+
 def test_run_to_run_bit_identity(eng):
     import torch
 
