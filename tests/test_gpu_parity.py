@@ -536,3 +536,54 @@ def test_anti_restate_guard(eng, V):
     assert [anti_restate_select(g[b], hists[b], dec) for b in range(B)] == want
     with pytest.raises(Exception):
         eng.sample_batch(x, params, histories=hists, sync=False)
+
+
+def test_decode_step_in_a_graph(eng):
+    # A decode step with every input on the device (RNG states, history ring,
+    # logits) captured into a HIP graph and replayed: each replay must give
+    # the tokens and state of the same step run eagerly, with eager work
+    # (new logits, readbacks, synchronizations) between the replays
+    import torch
+    from lumen_amd.sampling import DeviceDecodeState
+
+    B, V, steps = 4, 50_000, 8
+    rng = np.random.default_rng(23)
+    params = [SP(temperature=0.8, top_p=0.9, repetition_penalty=1.2, repeat_last_n=16),
+              SP(temperature=0.0, frequency_penalty=0.5),
+              SP(temperature=1.0, top_k=40, presence_penalty=0.4),
+              SP(temperature=0.7)]
+    seeds = [5, 6, 7, 8]
+    prompts = [rng.integers(0, V, size=n).astype(np.uint32) for n in (3, 0, 10, 1)]
+    seq = [torch.from_numpy((rng.standard_normal((B, V)) * 3).astype(np.float32)).cuda()
+           for _ in range(steps)]
+    x = torch.empty((B, V), dtype=torch.float32, device="cuda:0")
+    # eager
+    de = DeviceDecodeState(seeds, cap=256, histories=prompts)
+    te = torch.empty(B, dtype=torch.int32, device="cuda:0")
+    want = []
+    for st in range(steps):
+        x.copy_(seq[st])
+        de.step(eng, x, params, tokens_out=te, sync=False)
+        want.append(te.cpu().tolist())
+    # warm-up on a throwaway state (the context allocates its buffers here),
+    # then capture one step of a fresh state
+    dw = DeviceDecodeState(seeds, cap=256, histories=prompts)
+    dg = DeviceDecodeState(seeds, cap=256, histories=prompts)
+    tg = torch.empty(B, dtype=torch.int32, device="cuda:0")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dw.step(eng, x, params, tokens_out=tg, sync=False)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    log(f"case graph capture B={B} V={V}")
+    with torch.cuda.graph(g):
+        dg.step(eng, x, params, tokens_out=tg, sync=False)
+    for st in range(steps):
+        x.copy_(seq[st])
+        g.replay()
+        torch.cuda.synchronize()
+        assert tg.cpu().tolist() == want[st], f"replay {st}"
+    assert torch.equal(dg.rng, de.rng) and torch.equal(dg.ring, de.ring)
+    assert torch.equal(dg.lens, de.lens)
