@@ -23,6 +23,8 @@ The JSON line also carries:
                 sequential draws (launch + 4-byte readback + sync)
   b1_decode_device_state  the same as a decode loop with the RNG state and
                 the history on the device (no host draw, no history upload)
+  b1_graph_decode  those decode steps captured 32 to a HIP graph: time per
+                token without host work between steps
 """
 import argparse
 import json
@@ -190,6 +192,40 @@ def b1_decode_device_state(eng, draws=2_000):
     return float(np.percentile(times, 50)), float(np.percentile(times, 99)), len(times)
 
 
+def b1_graph_decode(eng, per_graph=32, replays=20):
+    """Config 2 decode steps with the state on the device, captured in one
+    HIP graph of `per_graph` consecutive steps: GPU time per token with no
+    host work between steps."""
+    import torch
+
+    from lumen_amd.sampling import DeviceDecodeState
+    from lumen_amd.workloads import config2
+
+    w = config2()
+    dev = torch.from_numpy(w.logits).cuda()
+    tok = torch.empty(1, dtype=torch.int32, device=dev.device)
+    warm = DeviceDecodeState(w.seeds, cap=8192, histories=w.histories)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        warm.step(eng, dev, w.params, tokens_out=tok, sync=False)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    ds = DeviceDecodeState(w.seeds, cap=8192, histories=w.histories)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            ds.step(eng, dev, w.params, tokens_out=tok, sync=False)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        g.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return dt / (replays * per_graph) * 1e6, replays * per_graph
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -285,6 +321,11 @@ def main():
         line["b1_latency"] = {"p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
                               "workload": "config2: B=1 V=248320 f32, top_k 20 top_p 0.8 "
                                           "presence 1.5 frequency 0.5"}
+        us, n = b1_graph_decode(eng)
+        line["b1_graph_decode"] = {
+            "us_per_token": round(us, 2), "tokens": n,
+            "workload": "config2 decode steps (device RNG and history ring) captured 32 to a "
+                        "HIP graph; wall time per token over graph replays"}
         p50, p99, n = b1_decode_device_state(eng)
         line["b1_decode_device_state"] = {
             "p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
