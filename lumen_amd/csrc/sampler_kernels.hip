@@ -2828,75 +2828,100 @@ __device__ __forceinline__ float chain_walk(const KernelArgs& a, int b, uint32_t
   const uint32_t nslots = G * (uint32_t)kChainMaxQ * (uint32_t)kWaves;
   const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
   const uint32_t* woff = s.H + 1024;
-  if (t < 64u) {
-    const uint32_t lane = t;
-    float c = 0.f;
-    uint32_t nre = 0;
-    for (uint32_t s0 = 0; s0 < nslots; s0 += 64u) {
-      const uint32_t sj = s0 + lane;
-      uint32_t wo = kSlotAbsent, nb = 0, sb = kEmptyRun, a0 = 0, a1 = 0;
-      if (sj < nslots) {
-        wo = woff[sj];
-        if (wo < kSlotAbsent) {
-          nb = words[wo];
-          sb = words[wo + 1];
-          a0 = words[wo + 2];
-          a1 = words[wo + 3];
+  // Wave 0 walks from slot `from` until the end or a record it cannot use;
+  // such a segment is then summed again by the whole workgroup, and the
+  // walk resumes after it.
+  uint32_t from = 0, nre = 0, nbw = 0;
+  float c = 0.f;
+  for (;;) {
+    if (t < 64u) {
+      const uint32_t lane = t;
+      uint32_t stop = 0xffffffffu;
+      for (uint32_t s0 = from; s0 < nslots && stop == 0xffffffffu; s0 += 64u) {
+        const uint32_t sj = s0 + lane;
+        uint32_t wo = kSlotAbsent, nb = 0, sb = kEmptyRun, a0 = 0, a1 = 0;
+        if (sj < nslots) {
+          wo = woff[sj];
+          if (wo < kSlotAbsent) {
+            nb = words[wo];
+            sb = words[wo + 1];
+            a0 = words[wo + 2];
+            a1 = words[wo + 3];
+          }
         }
-      }
-      const bool present = wo != kSlotAbsent;
-      const bool simple = wo < kSlotAbsent && nb == 0u;
-      uint32_t t0 = 0;
-      for (;;) {
-        const uint32_t cb = __float_as_uint(c);
-        const uint32_t bin = cb & 0xff800000u;
-        const uint32_t ub = bin + 0x00800000u;
-        const bool act = lane >= t0 && present;
-        // an empty run (all-zero segment) is the identity in any binade
-        const bool fit = simple && (sb == bin || sb == kEmptyRun);
-        PMap m{0u, 0u};
-        if (act && fit && sb != kEmptyRun) m = PMap{a0, a1};
-        const PMap id{0u, 0u};
-        const PMap ex = wave_shr1(wave_scan_incl(m, id, pm_combine), id);
-        const uint32_t before = (cb & 1u) ? ex.a1 : ex.a0;
-        const uint32_t own = ((cb ^ before) & 1u) ? m.a1 : m.a0;
-        const uint32_t sbits = cb + before;
-        const uint32_t ebits = sbits + own;
-        const bool bad = act && (!fit || before >= kSat || own >= kSat || ebits >= ub);
-        const unsigned long long bm = __ballot(bad);
-        if (!bm) {
-          c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)ebits, 63));
-          break;
-        }
-        const int tb = __ffsll((long long)bm) - 1;
-        c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)sbits, tb));
-        const uint32_t wt = (uint32_t)__builtin_amdgcn_readlane((int)wo, tb);
-        const bool ok = wt < kSlotAbsent && rec_walk<M>(words + wt, c);
-        if (!ok) {
+        const bool present = wo != kSlotAbsent;
+        const bool simple = wo < kSlotAbsent && nb == 0u;
+        uint32_t t0 = 0;
+        for (;;) {
+          const uint32_t cb = __float_as_uint(c);
+          const uint32_t bin = cb & 0xff800000u;
+          const uint32_t ub = bin + 0x00800000u;
+          const bool act = lane >= t0 && present;
+          // an empty run (all-zero segment) is the identity in any binade
+          const bool fit = simple && (sb == bin || sb == kEmptyRun);
+          PMap m{0u, 0u};
+          if (act && fit && sb != kEmptyRun) m = PMap{a0, a1};
+          const PMap id{0u, 0u};
+          const PMap ex = wave_shr1(wave_scan_incl(m, id, pm_combine), id);
+          const uint32_t before = (cb & 1u) ? ex.a1 : ex.a0;
+          const uint32_t own = ((cb ^ before) & 1u) ? m.a1 : m.a0;
+          const uint32_t sbits = cb + before;
+          const uint32_t ebits = sbits + own;
+          const bool bad = act && (!fit || before >= kSat || own >= kSat || ebits >= ub);
+          const unsigned long long bm = __ballot(bad);
+          if (!bm) {
+            c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)ebits, 63));
+            break;
+          }
+          const int tb = __ffsll((long long)bm) - 1;
+          c = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)sbits, tb));
+          const uint32_t wt = (uint32_t)__builtin_amdgcn_readlane((int)wo, tb);
+          float y = c;
+          ++nbw;
+          if (wt < kSlotAbsent && rec_walk<M>(words + wt, y)) {
+            c = y;
+          } else {
 #ifdef LUMEN_DEBUG_RECORDS
-          if (lane == 0 && b == 0)
-            printf("walk: slot %u %s at c=%a (nb %u)\n", s0 + (uint32_t)tb,
-                   wt >= kSlotAbsent ? "missing" : "mismatch", c,
-                   wt < kSlotAbsent ? words[wt] : 0u);
+            if (lane == 0 && b == 0)
+              printf("walk: slot %u %s at c=%a (nb %u)\n", s0 + (uint32_t)tb,
+                     wt >= kSlotAbsent ? "missing" : "mismatch", c,
+                     wt < kSlotAbsent ? words[wt] : 0u);
 #endif
-          c = seg_recompute<M>(row, rec_range<M>(V, G, s0 + (uint32_t)tb), m1, c);
-          ++nre;
-          LUMEN_TICK("walk_recomputed", b);
+            stop = s0 + (uint32_t)tb;  // c is its exact start
+            break;
+          }
+          t0 = (uint32_t)tb + 1u;
+          if (t0 >= 64u) break;
         }
-        t0 = (uint32_t)tb + 1u;
-        if (t0 >= 64u) break;
+      }
+      if (lane == 0) {
+        s.red_f[0] = c;
+        s.misc_u[3] = stop;
+        s.misc_u[2] = nbw;
       }
     }
-    if (lane == 0) {
-      s.red_f[0] = c;
-      s.misc_i[0] = (int)nre;
+    __syncthreads();
+    c = s.red_f[0];
+    const uint32_t stop = s.misc_u[3];
+    __syncthreads();
+    if (stop == 0xffffffffu) break;
+    // the segment again, by the whole workgroup: two summands per thread
+    const Slice r = rec_range<M>(V, G, stop);
+    static_assert(64 * M <= 2 * kThreads, "a segment fits two summands per thread");
+    float x[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t i = r.lo + 2u * t + (uint32_t)q;
+      x[q] = i < r.hi ? expf_glibc(__fsub_rn(row.at(i), m1)) : 0.f;
     }
+    c = ecss_fast_chunk<2>(c, x, kEcssSum, 0.f, s.ecss, s.est, s.wsum,
+                           (int)min((uint32_t)kThreads, (r.hi - r.lo + 1u) / 2u)).c;
+    ++nre;
+    LUMEN_TICK("walk_recomputed", b);
+    from = stop + 1u;
   }
-  __syncthreads();
-  const float S1 = s.red_f[0];
-  *nre_out = (uint32_t)s.misc_i[0];
-  __syncthreads();
-  return S1;
+  *nre_out = nre | (s.misc_u[2] << 8);
+  return c;
 }
 
 // After the row barrier (m1 known): this workgroup's candidates, still in
@@ -3073,7 +3098,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   tr.path = 4u;
   tr.passes = 2;
   tr.topp_sum = S1;
-  tr.pad[0] = nre;  // diagnostics: segments summed again by the walk
+  tr.pad[0] = nre;  // diagnostics: segments summed again | records walked one by one << 8
   topp_window(a, b, P, row, m1, S1, tau, ncand, rdraw, s, tr);
 }
 
