@@ -149,6 +149,10 @@ class Engine:
         except Exception:
             pass
 
+    def prepare(self, logits, params: Sequence[SamplingParams], **kw) -> "PreparedBatch":
+        """A reusable batch description (see PreparedBatch)."""
+        return PreparedBatch(self, logits, params, **kw)
+
     def sample_batch(self, logits, params: Sequence[SamplingParams],
                      histories: Optional[Sequence[Sequence[int]]] = None,
                      uniforms: Optional[Sequence[float]] = None,
@@ -316,6 +320,79 @@ class DeviceDecodeState:
     def step(self, eng: "Engine", logits, params: Sequence[SamplingParams], **kw):
         return eng.sample_batch(logits, params, rng_states_dev=self.rng,
                                 hist_ring_dev=self.ring, hist_len_dev=self.lens, **kw)
+
+
+class PreparedBatch:
+    """A batch whose C description is built once and reused across calls:
+    the decode-loop form of Engine.sample_batch. Between calls only the
+    per-row draws change (`run(uniforms)`); the logits, parameters, penalty
+    counts and outputs are the tensors given here, read again on every call
+    (update them in place). The per-call host cost is one C-ABI call."""
+
+    def __init__(self, eng: "Engine", logits, params: Sequence[SamplingParams],
+                 penalty_counts=None, tokens_out=None, trace=None, stream=None,
+                 uniforms_dev=None, rng_states_dev=None):
+        import torch
+
+        lg, dt = _as_device_logits(logits)
+        B, V = lg.shape
+        if len(params) != B:
+            raise ValueError("one SamplingParams per row")
+        self._eng = eng
+        self._keep = [lg]
+        self.params_c = (_native.SamplingParamsC * B)(*[p.to_c() for p in params])
+        bt = _native.BatchC()
+        bt.logits = lg.data_ptr()
+        bt.dtype = dt
+        bt.batch = B
+        bt.vocab = V
+        bt.row_stride = lg.stride(0) if B > 1 else V
+        bt.params = self.params_c
+        if penalty_counts is not None:
+            offs, ids, cnts = penalty_counts
+            self._keep += [offs, ids, cnts]
+            bt.pen_offsets = offs.data_ptr()
+            bt.pen_ids = ids.data_ptr()
+            bt.pen_counts = cnts.data_ptr()
+        self.uniforms = np.zeros(B, dtype=np.float32)
+        if uniforms_dev is not None:
+            self._keep.append(uniforms_dev)
+            bt.uniforms_dev = uniforms_dev.data_ptr()
+        elif rng_states_dev is not None:
+            self._keep.append(rng_states_dev)
+            bt.rng_states_dev = rng_states_dev.data_ptr()
+        else:
+            bt.uniforms = self.uniforms.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+        if tokens_out is None:
+            tokens_out = torch.empty(B, dtype=torch.int32, device=lg.device)
+        self.tokens = tokens_out
+        bt.tokens = tokens_out.data_ptr()
+        if trace is not None:
+            self._keep.append(trace)
+            bt.trace = trace.data_ptr()
+        self._bt = bt
+        self._bref = ctypes.byref(bt)
+        self._host = (ctypes.c_uint32 * B)()
+        self._stream = stream if stream is not None else \
+            torch.cuda.current_stream(lg.device).cuda_stream
+        L = _native.load()
+        self._sync = L.lumen_sampler_sample_batch_sync
+        self._async = L.lumen_sampler_sample_batch
+
+    def run(self, uniforms: Optional[Sequence[float]] = None, sync: bool = True):
+        """One call. uniforms: this call's draws (host form only); returns the
+        host token list (sync) or None (the tokens are in `self.tokens`)."""
+        if uniforms is not None:
+            self.uniforms[:] = uniforms
+        if sync:
+            rc = self._sync(self._eng._h, self._bref, self._host, self._stream)
+            if rc:
+                _native.check(rc, "lumen_sampler_sample_batch_sync")
+            return list(self._host)
+        rc = self._async(self._eng._h, self._bref, self._stream)
+        if rc:
+            _native.check(rc, "lumen_sampler_sample_batch")
+        return None
 
 
 _engines: Dict[int, Engine] = {}

@@ -587,3 +587,28 @@ def test_decode_step_in_a_graph(eng):
         assert tg.cpu().tolist() == want[st], f"replay {st}"
     assert torch.equal(dg.rng, de.rng) and torch.equal(dg.ring, de.ring)
     assert torch.equal(dg.lens, de.lens)
+
+
+def test_prepared_batch_matches_sample_batch(eng):
+    # Engine.prepare builds the C description once; each run() must give what
+    # sample_batch gives for the same draws, sync and async
+    import torch
+    from lumen_amd.sampling import Xorshift64
+
+    rng = np.random.default_rng(31)
+    B, V = 3, 20_000
+    x = torch.from_numpy((rng.standard_normal((B, V)) * 2).astype(np.float32)).cuda()
+    params = [SP(temperature=0.7, top_k=20, top_p=0.8), SP(temperature=0.0),
+              SP(temperature=1.2, min_p=0.05)]
+    pb = eng.prepare(x, params)
+    r = Xorshift64(5)
+    for call in range(6):
+        u = [r.next_f32() for _ in range(B)]
+        _, want = eng.sample_batch(x, params, uniforms=u)
+        if call % 2:
+            assert pb.run(u, sync=False) is None
+            torch.cuda.synchronize()
+            got = pb.tokens.cpu().tolist()
+        else:
+            got = pb.run(u)
+        assert got == want, f"call {call}"
