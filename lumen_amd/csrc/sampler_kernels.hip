@@ -1918,29 +1918,52 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
           break;
         }
         // probability window [p_lo, p_hi)
-        const float vL = key2f(L);
-        const float p_lo = (L == 0u) ? 0.f : __fdiv_rn(expf_glibc(__fsub_rn(vL, m1)), S1);
         const float vH = key_hi >= (1ull << 32) ? __uint_as_float(0x7f800000u) : key2f((uint32_t)key_hi);
-        const float dl = __fadd_rn(__fmul_rn(fabsf(vL) + fabsf(m1), 0x1p-12f), 0x1p-20f);
         const float dh = __fadd_rn(__fmul_rn(fabsf(vH) + fabsf(m1), 0x1p-12f), 0x1p-20f);
-        const float lo_v = (L == 0u) ? kNegInf : __fsub_rn(vL, dl);
         const float hi_v = __fadd_rn(vH, dh);
-        if (t == 0) s.cnt = 0;
-        __syncthreads();
-        row_foreach(row, [&](uint32_t i, float v) {
-          float x = v1f(v);
-          bool in = false;
-          uint32_t pb = 0;
-          if (x >= lo_v && x <= hi_v) {
-            float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
-            in = p > 0.f && p >= p_lo && p < p_hi;
-            pb = __float_as_uint(p);
+        float p_lo = 0.f;
+        uint32_t n = 0;
+        for (;;) {
+          const float vL = key2f(L);
+          p_lo = (L == 0u) ? 0.f : __fdiv_rn(expf_glibc(__fsub_rn(vL, m1)), S1);
+          const float dl = __fadd_rn(__fmul_rn(fabsf(vL) + fabsf(m1), 0x1p-12f), 0x1p-20f);
+          const float lo_v = (L == 0u) ? kNegInf : __fsub_rn(vL, dl);
+          if (t == 0) s.cnt = 0;
+          __syncthreads();
+          row_foreach(row, [&](uint32_t i, float v) {
+            float x = v1f(v);
+            bool in = false;
+            uint32_t pb = 0;
+            if (x >= lo_v && x <= hi_v) {
+              float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
+              in = p > 0.f && p >= p_lo && p < p_hi;
+              pb = __float_as_uint(p);
+            }
+            list_push(s.Bk, &s.cnt, in, ((uint64_t)(~pb) << 32) | i);
+          });
+          __syncthreads();
+          tr.passes++;
+          n = s.cnt;
+          if (n <= (uint32_t)kCap || L == 0u) break;
+          // The tokens with p == p_lo reach below the planned edge L (values
+          // under vL whose probability rounds to the same p, such as the
+          // subnormals around zero): move the edge up to the first key whose
+          // p exceeds p_lo, which leaves that whole group to the next window.
+          if (t == 0) {
+            uint64_t lo = (uint64_t)L + 1u, hi = key_hi;
+            while (lo < hi) {
+              const uint64_t mid = (lo + hi) >> 1;
+              const float pm = __fdiv_rn(expf_glibc(__fsub_rn(key2f((uint32_t)mid), m1)), S1);
+              if (pm > p_lo) hi = mid; else lo = mid + 1u;
+            }
+            s.misc_u[0] = lo < key_hi ? (uint32_t)lo : 0u;
           }
-          list_push(s.Bk, &s.cnt, in, ((uint64_t)(~pb) << 32) | i);
-        });
-        __syncthreads();
-        tr.passes++;
-        const uint32_t n = s.cnt;
+          __syncthreads();
+          const uint32_t up = s.misc_u[0];
+          __syncthreads();
+          if (up == 0u) break;  // one probability group fills the window: overflow below
+          L = up;
+        }
         if (n > (uint32_t)kCap) {
           tr.status = kStatusListOverflow;
           break;

@@ -154,6 +154,52 @@ def test_random_small_vocab(eng, V):
              check_pen=True)
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("V,dtype", [(151_936, "f32"), (248_320, "f32"), (151_936, "bf16")])
+def test_random_full_vocab(eng, V, dtype, seed):
+    # random parameter mixes over full-size rows: every split path and its
+    # fallbacks, the weighted block plan of a mixed batch, penalties from
+    # random histories, and bf16 rows
+    from lumen_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(V + (7 if dtype == "bf16" else 0) + 1000 * seed)
+    B = 24
+    lg = np.stack([random_logits(rng, V, b % 6) for b in range(B)])
+    params = []
+    for _ in range(B):
+        p = random_params(rng, V)
+        if p.top_k is not None and p.top_k > V:
+            p.top_k = int(rng.choice([50, 1024, 3000]))
+        params.append(p)
+    hists = [rng.integers(0, V, int(rng.integers(0, 3000))).astype(np.uint32) for _ in range(B)]
+    u = rng.random(B).astype(np.float32)
+    log(f"case random full V={V} {dtype} seed {seed}")
+    if dtype == "bf16":
+        bits = to_bf16_bits(lg)
+        f32 = (bits.astype(np.uint32) << 16).view(np.float32)
+        rep = parity.compare(eng, f32, params, hists, u, dtype="bf16", bf16_bits=bits)
+    else:
+        rep = parity.compare(eng, lg, params, hists, u)
+    assert_clean(rep, f"random full V={V} {dtype}")
+
+
+def test_window_edge_probability_ties(eng):
+    # Logits on a 1/4 grid with ~7,500 exact zeros: a top-p window edge
+    # planned between +0 and the smallest subnormal key leaves the zeros,
+    # whose p equals the edge's, below the edge. The window must move its
+    # edge up rather than overflow (this once reported a row failure).
+    rng = np.random.default_rng(77)
+    V, B = 151_936, 4
+    lg = (np.round(rng.normal(0, 2, (B, V)) * 4) / 4).astype(np.float32)
+    params = [SP(temperature=1.5, top_p=0.999, presence_penalty=1.5),
+              SP(temperature=1.0, top_p=0.9999),
+              SP(temperature=0.7, top_p=0.99999, min_p=0.001),
+              SP(temperature=1.0, top_p=0.999, top_k=3000)]
+    hists = [rng.integers(0, V, 89).astype(np.uint32), np.zeros(0, np.uint32),
+             np.zeros(0, np.uint32), rng.integers(0, V, 10).astype(np.uint32)]
+    run_case(eng, lg, params, hists, rng.random(B).astype(np.float32), name="edge_ties")
+
+
 def test_special_values(eng):
     V = 300
     rows, params = [], []
