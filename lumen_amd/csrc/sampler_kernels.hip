@@ -1602,6 +1602,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
     const uint32_t pk = tkey(vf(i, v)) >> 16;
     if (pk >= pk_lo && pk <= pk_hi) atomicAdd(&s.H[2047u - (i >> sh)], 1u);
   });
+  __syncthreads();  // every wave's counts are in before the search reads them
   tr.passes++;
   uint32_t ab = 0;
   const int d = find_from_top(s.H, 2048, k, &ab, s);
@@ -1634,6 +1635,51 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
   __syncthreads();
   LUMEN_TICK("bv_istar", 0);
   return 1;
+}
+
+// The k-th smallest id (k >= 1) among the tokens i with pred(i, x), x the
+// token's value through vf: an id histogram (lowest ids at the top of s.H)
+// finds the bin, a bitmap of the bin (s.H + 2048) the id. Two passes.
+template <class VF, class Pred>
+__device__ __forceinline__ uint32_t kth_id_where(const Row& row, VF&& vf, Pred&& pred, uint32_t k,
+                                                 Smem& s) {
+  const uint32_t t = threadIdx.x, V = row.V;
+  uint32_t sh = 0;
+  while ((V - 1u) >> sh >= 2048u) ++sh;  // bins of at most 2048 ids (V <= 2^22)
+  clear_hist(s.H, 2048);
+  __syncthreads();
+  row_foreach(row, [&](uint32_t i, float v) {
+    if (pred(i, vf(i, v))) atomicAdd(&s.H[2047u - (i >> sh)], 1u);
+  });
+  __syncthreads();  // every wave's counts are in before the search reads them
+  uint32_t ab = 0;
+  const int d = find_from_top(s.H, 2048, k, &ab, s);
+  const uint32_t lo = (2047u - (uint32_t)(d < 0 ? 0 : d)) << sh, hi = min(V, lo + (1u << sh));
+  uint32_t* bits = s.H + 2048;
+  for (uint32_t i = t; i < 64u; i += kThreads) bits[i] = 0u;
+  __syncthreads();
+  range_foreach(row, lo, hi, [&](uint32_t i, float v) {
+    if (pred(i, vf(i, v))) atomicOr(&bits[(i - lo) >> 5], 1u << ((i - lo) & 31u));
+  });
+  __syncthreads();
+  if (t == 0) {
+    uint32_t left = k - ab, id = lo;
+    for (uint32_t w = 0; w < 64u; ++w) {
+      const uint32_t n = __popc(bits[w]);
+      if (left <= n) {
+        uint32_t m = bits[w];
+        for (uint32_t q = 1; q < left; ++q) m &= m - 1u;
+        id = lo + w * 32u + (uint32_t)(__ffs(m) - 1);
+        break;
+      }
+      left -= n;
+    }
+    s.misc_u[2] = id;
+  }
+  __syncthreads();
+  const uint32_t id = s.misc_u[2];
+  __syncthreads();
+  return id;
 }
 
 // The whole sampler for row b, run by one workgroup (used directly when a
@@ -1867,6 +1913,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
         // plan the next window [L, key_hi) of at most kCapWindow keys
         uint32_t L = 0;
         bool empty = false, overflow = false;
+        uint32_t gkey = 0;  // overflow: the one key that holds more than a window
         {
           uint32_t pre = 0, pm = 0;
           bool decided = false;
@@ -1909,65 +1956,139 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
             }
             __syncthreads();
           }
-          if (!decided) overflow = true;  // more than a window of one exact key
+          if (!decided) {
+            overflow = true;  // more than a window of one exact key
+            gkey = pre;
+          }
         }
         if (empty) break;
-        if (!overflow && (uint64_t)L >= key_hi) overflow = true;  // no progress: never loop
-        if (overflow || tr.windows >= 4096u) {
-          tr.status = kStatusTieOverflow;
+        if ((!overflow && (uint64_t)L >= key_hi) || tr.windows >= 4096u) {
+          tr.status = kStatusTieOverflow;  // no progress: never loop
           break;
         }
-        // probability window [p_lo, p_hi)
-        const float vH = key_hi >= (1ull << 32) ? __uint_as_float(0x7f800000u) : key2f((uint32_t)key_hi);
-        const float dh = __fadd_rn(__fmul_rn(fabsf(vH) + fabsf(m1), 0x1p-12f), 0x1p-20f);
-        const float hi_v = __fadd_rn(vH, dh);
+        bool as_group = overflow;
         float p_lo = 0.f;
         uint32_t n = 0;
-        for (;;) {
-          const float vL = key2f(L);
-          p_lo = (L == 0u) ? 0.f : __fdiv_rn(expf_glibc(__fsub_rn(vL, m1)), S1);
-          const float dl = __fadd_rn(__fmul_rn(fabsf(vL) + fabsf(m1), 0x1p-12f), 0x1p-20f);
-          const float lo_v = (L == 0u) ? kNegInf : __fsub_rn(vL, dl);
-          if (t == 0) s.cnt = 0;
-          __syncthreads();
+        if (!as_group) {
+          // probability window [p_lo, p_hi)
+          const float vH = key_hi >= (1ull << 32) ? __uint_as_float(0x7f800000u) : key2f((uint32_t)key_hi);
+          const float dh = __fadd_rn(__fmul_rn(fabsf(vH) + fabsf(m1), 0x1p-12f), 0x1p-20f);
+          const float hi_v = __fadd_rn(vH, dh);
+          for (;;) {
+            const float vL = key2f(L);
+            p_lo = (L == 0u) ? 0.f : __fdiv_rn(expf_glibc(__fsub_rn(vL, m1)), S1);
+            const float dl = __fadd_rn(__fmul_rn(fabsf(vL) + fabsf(m1), 0x1p-12f), 0x1p-20f);
+            const float lo_v = (L == 0u) ? kNegInf : __fsub_rn(vL, dl);
+            if (t == 0) s.cnt = 0;
+            __syncthreads();
+            row_foreach(row, [&](uint32_t i, float v) {
+              float x = v1f(v);
+              bool in = false;
+              uint32_t pb = 0;
+              if (x >= lo_v && x <= hi_v) {
+                float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
+                in = p > 0.f && p >= p_lo && p < p_hi;
+                pb = __float_as_uint(p);
+              }
+              list_push(s.Bk, &s.cnt, in, ((uint64_t)(~pb) << 32) | i);
+            });
+            __syncthreads();
+            tr.passes++;
+            n = s.cnt;
+            if (n <= (uint32_t)kCap || L == 0u) break;
+            // The tokens with p == p_lo reach below the planned edge L (values
+            // under vL whose probability rounds to the same p, such as the
+            // subnormals around zero): move the edge up to the first key whose
+            // p exceeds p_lo, which leaves that whole group to the next window.
+            if (t == 0) {
+              uint64_t lo = (uint64_t)L + 1u, hi = key_hi;
+              while (lo < hi) {
+                const uint64_t mid = (lo + hi) >> 1;
+                const float pm = __fdiv_rn(expf_glibc(__fsub_rn(key2f((uint32_t)mid), m1)), S1);
+                if (pm > p_lo) hi = mid; else lo = mid + 1u;
+              }
+              s.misc_u[0] = lo < key_hi ? (uint32_t)lo : 0u;
+            }
+            __syncthreads();
+            const uint32_t up = s.misc_u[0];
+            __syncthreads();
+            if (up == 0u) {
+              // every key of the window shares one p: a probability group
+              // larger than a window, summed as repeated adds below
+              as_group = true;
+              gkey = L;
+              break;
+            }
+            L = up;
+          }
+          if (!as_group && n > (uint32_t)kCap) {
+            tr.status = kStatusListOverflow;
+            break;
+          }
+        }
+        if (as_group) {
+          // The top remaining probability group (one key, or neighbouring
+          // keys whose p rounds equal) holds more tokens than a window: the
+          // group is one summand repeated (rep_replay), and a crossing inside
+          // it keeps the group's lowest ids (sampling.rs:948-960: ties in p
+          // are sorted by id).
+          const float vK = key2f(gkey);
+          const float pg = __fdiv_rn(expf_glibc(__fsub_rn(vK, m1)), S1);
+          if (!(pg > 0.f)) break;  // zero probabilities never reach top_p
+          const float dK = __fadd_rn(__fmul_rn(fabsf(vK) + fabsf(m1), 0x1p-12f), 0x1p-20f);
+          const float glo = __fsub_rn(vK, dK), ghi = __fadd_rn(vK, dK);
+          const uint64_t khi = key_hi;
+          auto ingroup = [&](uint32_t, float x) {
+            return x >= glo && x <= ghi && (uint64_t)tkey(x) < khi &&
+                   __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1) == pg;
+          };
+          uint32_t ng = 0, kmin = 0xffffffffu;
           row_foreach(row, [&](uint32_t i, float v) {
-            float x = v1f(v);
-            bool in = false;
-            uint32_t pb = 0;
-            if (x >= lo_v && x <= hi_v) {
-              float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
-              in = p > 0.f && p >= p_lo && p < p_hi;
-              pb = __float_as_uint(p);
+            const float x = v1f(v);
+            if (ingroup(i, x)) {
+              ++ng;
+              kmin = min(kmin, tkey(x));
             }
-            list_push(s.Bk, &s.cnt, in, ((uint64_t)(~pb) << 32) | i);
           });
-          __syncthreads();
           tr.passes++;
-          n = s.cnt;
-          if (n <= (uint32_t)kCap || L == 0u) break;
-          // The tokens with p == p_lo reach below the planned edge L (values
-          // under vL whose probability rounds to the same p, such as the
-          // subnormals around zero): move the edge up to the first key whose
-          // p exceeds p_lo, which leaves that whole group to the next window.
-          if (t == 0) {
-            uint64_t lo = (uint64_t)L + 1u, hi = key_hi;
-            while (lo < hi) {
-              const uint64_t mid = (lo + hi) >> 1;
-              const float pm = __fdiv_rn(expf_glibc(__fsub_rn(key2f((uint32_t)mid), m1)), S1);
-              if (pm > p_lo) hi = mid; else lo = mid + 1u;
+          ng = block_sum_u32(ng, s);
+          kmin = ~(uint32_t)block_max_u64((uint64_t)(~kmin), s);
+          if (!(pg < p_hi)) {
+            // the group was summed with the window above (it gathers by p)
+            key_hi = kmin;
+            continue;
+          }
+          if (t < 64u) {
+            float y = c, prev = c;
+            uint32_t j = 0;
+            const bool f = rep_replay(y, prev, pg, ng, P.top_p, true, j);
+            if (t == 0) {
+              s.red_f[0] = y;
+              s.misc_u[0] = f ? 1u : 0u;
+              s.misc_u[1] = j;
             }
-            s.misc_u[0] = lo < key_hi ? (uint32_t)lo : 0u;
           }
           __syncthreads();
-          const uint32_t up = s.misc_u[0];
+          const float y = s.red_f[0];
+          const bool hitg = s.misc_u[0] != 0u;
+          const uint32_t jg = s.misc_u[1];
           __syncthreads();
-          if (up == 0u) break;  // one probability group fills the window: overflow below
-          L = up;
-        }
-        if (n > (uint32_t)kCap) {
-          tr.status = kStatusListOverflow;
-          break;
-        }
+          tr.windows++;
+          if (hitg) {
+            found = true;
+            pstar = pg;
+            istar = kth_id_where(row, [&](uint32_t, float v) { return v1f(v); }, ingroup, jg + 1u, s);
+            tr.topp_kept = ranks + jg + 1u;
+            tr.topp_cum = y;
+            pmode = 2;
+            break;
+          }
+          c = y;
+          ranks += ng;
+          key_hi = kmin;
+          p_hi = pg;
+          continue;
+                }
         tr.windows++;
         sort_u64_asc(s.Bk, n, s.A, s);
         EcssResult w = list_ecss(

@@ -183,6 +183,54 @@ def test_random_full_vocab(eng, V, dtype, seed):
     assert_clean(rep, f"random full V={V} {dtype}")
 
 
+@pytest.mark.parametrize("B,seed", [(1, 0), (1, 1), (1, 2), (5, 0), (5, 1), (64, 0), (64, 1)])
+def test_random_full_vocab_batch_sizes(eng, B, seed):
+    # batch sizes that change the grid: 16 slices per row (B = 1, 5), the
+    # weighted block plan (B = 64)
+    rng = np.random.default_rng(10_000 + 100 * B + seed)
+    V = 248_320
+    lg = np.stack([random_logits(rng, V, int(rng.integers(0, 6))) for b in range(B)])
+    params = []
+    for _ in range(B):
+        p = random_params(rng, V)
+        if p.top_k is not None and p.top_k > V:
+            p.top_k = int(rng.choice([20, 500, 2048, 4000]))
+        params.append(p)
+    hists = [rng.integers(0, V, int(rng.integers(0, 5000))).astype(np.uint32) for _ in range(B)]
+    run_case(eng, lg, params, hists, rng.random(B).astype(np.float32),
+             name=f"random B={B} seed {seed}")
+
+
+def test_huge_tie_groups(eng):
+    # probability groups larger than a window: one value repeated 20,000
+    # times with the top-p crossing inside the group (its lowest ids are
+    # kept), +0 and -0 together (two keys, one p), and groups above and below
+    # the crossing
+    rng = np.random.default_rng(91)
+    V = 248_320
+    rows, params = [], []
+    r = rng.normal(0, 1, V).astype(np.float32)
+    r[rng.choice(V, 20_000, replace=False)] = 1.0
+    rows.append(r)
+    params.append(SP(temperature=1.0, top_p=0.5))
+    r = (np.round(rng.normal(0, 2, V) * 4) / 4).astype(np.float32)  # +0 and -0: ~12K tokens
+    rows.append(r)
+    params.append(SP(temperature=0.9, top_p=0.995))
+    r = np.zeros(V, np.float32)
+    r[: V // 2] = -0.0
+    r[rng.choice(V, 30, replace=False)] = 3.0
+    rows.append(r)
+    params.append(SP(temperature=1.0, top_p=0.3))
+    r = rng.integers(-3, 4, V).astype(np.float32)  # 7 values, ~35K tokens each
+    rows.append(r)
+    params.append(SP(temperature=1.2, top_p=0.97, min_p=0.01))
+    B = len(rows)
+    lg = np.stack(rows)
+    for draws in (rng.random(B), np.full(B, 0.9999)):
+        run_case(eng, lg, params, [np.zeros(0, np.uint32)] * B, draws.astype(np.float32),
+                 name="huge_ties")
+
+
 def test_window_edge_probability_ties(eng):
     # Logits on a 1/4 grid with ~7,500 exact zeros: a top-p window edge
     # planned between +0 and the smallest subnormal key leaves the zeros,
