@@ -201,6 +201,41 @@ def test_random_full_vocab_batch_sizes(eng, B, seed):
              name=f"random B={B} seed {seed}")
 
 
+@pytest.mark.parametrize("seed", list(range(12)))
+def test_fuzz_shapes(eng, seed):
+    # random vocabularies (unaligned sizes too), batch sizes, dtypes, row
+    # strides, logit styles and parameter mixes
+    from lumen_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(50_000 + seed)
+    V = int(rng.choice([100_003, 151_936, 200_001, 248_320, 262_139]))
+    B = int(rng.integers(1, 41))
+    bf16 = bool(rng.random() < 0.35)
+    lg = np.stack([random_logits(rng, V, int(rng.integers(0, 6))) for _ in range(B)])
+    params = []
+    for _ in range(B):
+        p = random_params(rng, V)
+        if p.top_k is not None and p.top_k > V:
+            p.top_k = int(rng.choice([1, 7, 64, 1000, 2048, 2049, 5000]))
+        if rng.random() < 0.15:
+            p.top_p = float(rng.choice([0.99999, 0.9999, 1e-6]))
+        if rng.random() < 0.1:
+            p.temperature = float(rng.choice([1e-4, 2.0, 1.9999]))
+        params.append(p)
+    hists = [rng.integers(0, V, int(rng.integers(0, 6000))).astype(np.uint32) for _ in range(B)]
+    u = rng.random(B).astype(np.float32)
+    stride = V + int(rng.choice([0, 0, 1, 7, 64]))
+    log(f"case fuzz seed {seed} B={B} V={V} bf16={bf16} stride={stride}")
+    if bf16:
+        bits = to_bf16_bits(lg)
+        f32 = (bits.astype(np.uint32) << 16).view(np.float32)
+        rep = parity.compare(eng, f32, params, hists, u, dtype="bf16", bf16_bits=bits,
+                             row_stride=stride)
+    else:
+        rep = parity.compare(eng, lg, params, hists, u, row_stride=stride)
+    assert_clean(rep, f"fuzz seed {seed}")
+
+
 def test_huge_tie_groups(eng):
     # probability groups larger than a window: one value repeated 20,000
     # times with the top-p crossing inside the group (its lowest ids are
