@@ -333,6 +333,19 @@ def main():
                      "kernel": "lumen_sample_rows", "kernel_ms": round(kern_ms, 5),
                      "bytes_per_launch": logit_bytes},
     }
+    # logit passes per row, from the row traces of one more call
+    trace = torch.zeros((B, 16), dtype=torch.int32, device=dev.device)
+    eng.sample_batch(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=tok,
+                     trace=trace, sync=False)
+    torch.cuda.synchronize()
+    passes = trace.cpu().numpy().view(np.uint32)[:, 13]
+    kinds = {}
+    for b, p in enumerate(w.params):
+        kind = ("greedy" if p.temperature <= 0 else
+                "+".join(k for k, on in (("top_k", p.top_k), ("top_p", p.top_p),
+                                          ("penalties", p.penalties_active())) if on) or "plain")
+        kinds.setdefault(kind, []).append(int(passes[b]))
+    line["logit_passes_per_row"] = {k: round(float(np.mean(v)), 2) for k, v in kinds.items()}
     if not args.no_b1:
         p50, p99, n, api50 = b1_latency(eng, args.b1_draws)
         line["b1_latency"] = {"p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
