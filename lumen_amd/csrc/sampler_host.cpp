@@ -470,6 +470,8 @@ void lumen_sampler_destroy(lumen_sampler* s) {
   if (s->cand.p) (void)hipFree(s->cand.p);
   if (s->est.p) (void)hipFree(s->est.p);
   if (s->hist.p) (void)hipFree(s->hist.p);
+  if (s->guard.p) (void)hipFree(s->guard.p);
+  if (s->wcnt.p) (void)hipFree(s->wcnt.p);
   if (s->staged) (void)hipEventDestroy(s->staged);
   if (s->module) (void)hipModuleUnload(s->module);
   if (s->map_host) (void)hipHostFree(s->map_host);
