@@ -64,13 +64,26 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
   const uint32_t gmin_topp =
       (V + 32u * kWgThreads * (uint32_t)lumen::kChainMaxQ - 1u) /
       (32u * kWgThreads * (uint32_t)lumen::kChainMaxQ);
+  // slice weights of the greedy, top-k and top-p paths; LUMEN_SAMPLER_WEIGHTS=g,k,p
+  // overrides them (a tuning aid)
+  struct Weights {
+    uint32_t g = 1, k = 2, p = 10;
+  };
+  static const Weights wt = [] {
+    Weights x;
+    if (const char* e = std::getenv("LUMEN_SAMPLER_WEIGHTS")) {
+      unsigned g = 0, k = 0, p = 0;
+      if (std::sscanf(e, "%u,%u,%u", &g, &k, &p) == 3 && g && k && p) x = Weights{g, k, p};
+    }
+    return x;
+  }();
   uint64_t wsum = 0;
   uint32_t fixed = 0;
   for (uint32_t b = 0; b < B; ++b) {
     switch (row_path(rows[b], V, lumen::kMaxSlices)) {
-      case kPathGreedy: w[b] = 1; break;
-      case kPathTopK: w[b] = 2; break;
-      case kPathTopP: w[b] = 10; break;
+      case kPathGreedy: w[b] = wt.g; break;
+      case kPathTopK: w[b] = wt.k; break;
+      case kPathTopP: w[b] = wt.p; break;
       default: w[b] = 0; ++fixed; break;  // exact single-workgroup row
     }
     wsum += w[b];
