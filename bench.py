@@ -252,6 +252,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-b1", action="store_true", help="skip the B=1 latency leg")
     ap.add_argument("--b1-draws", type=int, default=10_000)
+    ap.add_argument("--graph", type=int, default=10,
+                    help="also time the steps as replays of a HIP graph of this many launches")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (PMC calibration)")
     args = ap.parse_args()
@@ -296,6 +298,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # stream launches, one HIP-event pair per step
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     torch.cuda.synchronize()
@@ -305,8 +308,40 @@ def main():
         step()
         ends[i].record()
     torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    kern_ms = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
+    el_stream = time.perf_counter() - t0
+    kern_ms_stream = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
+    el, kern_ms, mode = el_stream, kern_ms_stream, "stream launches"
+    if args.graph > 1:
+        # The same K steps as replays of a HIP graph of `graph` sampler
+        # launches (parameters and draws are resident, so each launch records
+        # one kernel node and nothing else): the launch-bound loop captured,
+        # as a serving loop that captures its sampler runs it. Any remainder
+        # of K runs as stream launches inside the timed region.
+        pb = eng.prepare(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=tok)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            gpb = eng.prepare(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev,
+                              tokens_out=tok)
+            for _ in range(args.graph):
+                gpb.run(sync=False)
+        g.replay()
+        torch.cuda.synchronize()
+        reps, rem = divmod(args.steps, args.graph)
+        gs = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+        ge = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(reps):
+            gs[i].record()
+            g.replay()
+            ge[i].record()
+        for _ in range(rem):
+            pb.run(sync=False)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        if reps:
+            kern_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(gs, ge)])) / args.graph
+        mode = f"HIP graph replays of {args.graph} launches"
 
     logit_bytes = B * V * (2 if w.dtype == "bf16" else 4)
     achieved = logit_bytes / (kern_ms * 1e-3) / 1e9
@@ -327,6 +362,10 @@ def main():
         "config": {"workload": f"{w.name}: B={B} V={V} {w.dtype} logits, mixed sampling rows",
                    "batch": B, "vocab": V},
         "us_per_sample": round(el / args.steps / B * 1e6, 4),
+        "launch": mode,
+        "stream_launches": {"value": round(B * args.steps / el_stream, 1),
+                            "ms_per_step": round(el_stream / args.steps * 1e3, 4),
+                            "kernel_ms": round(kern_ms_stream, 5)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(f"lumen_sample_rows_{w.name}_pmc.txt"),
