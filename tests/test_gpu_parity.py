@@ -741,3 +741,48 @@ def test_prepared_batch_matches_sample_batch(eng):
         else:
             got = pb.run(u)
         assert got == want, f"call {call}"
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_anti_restate_fuzz(eng, seed):
+    # random greedy anti-restate rows (with and without penalties, windows,
+    # NaN / inf / tied logits, looping histories, random byte decoders)
+    # against the oracle's sample_logits, through the synchronous call
+    import torch
+    from lumen_amd.sampling import TokenBytes
+    from oracle import oracle as o
+
+    rng = np.random.default_rng(700 + seed)
+    V = int(rng.choice([97, 5000, 151_936]))
+    B = int(rng.integers(4, 24))
+    alpha = [b"a", b"b", b"ab", b" ", b"ba ", b"\t", b"abab", b"c"]
+    table = [b"".join(alpha[int(i)] for i in rng.integers(0, len(alpha), int(rng.integers(0, 4))))
+             for _ in range(V)]
+    dec = TokenBytes(table)
+    lg = np.stack([random_logits(rng, V, int(rng.integers(0, 6))) for _ in range(B)])
+    params, hists = [], []
+    for b in range(B):
+        loop = rng.integers(0, V, size=int(rng.integers(1, 6))).astype(np.uint32)
+        h = np.resize(loop, int(rng.integers(0, 40))).astype(np.uint32)
+        for j, tok in enumerate(np.unique(h)[:8]):
+            if rng.random() < 0.7:
+                lg[b, tok] = np.float32(lg[b].max() + 1.0 - 0.01 * j)
+        p = SP(temperature=0.0, anti_restate=True)
+        if rng.random() < 0.4:
+            p.repetition_penalty = float(rng.choice([1.1, 2.0]))
+            p.repeat_last_n = int(rng.choice([0, 3, 16]))
+        if rng.random() < 0.2:
+            p.frequency_penalty = 0.5
+        params.append(p)
+        hists.append(h)
+    x = torch.from_numpy(lg).to("cuda:0")
+    log(f"case anti_restate fuzz seed {seed} B={B} V={V}")
+    _, got = eng.sample_batch(x, params, histories=hists, decoder=dec)
+    want = []
+    for b in range(B):
+        p = params[b]
+        op = o.Params(temperature=0.0, anti_restate=True, repetition_penalty=p.repetition_penalty,
+                      repeat_last_n=p.repeat_last_n, frequency_penalty=p.frequency_penalty)
+        want.append(o.sample_logits(lg[b].copy(), op, hists[b], o.Xorshift64(1), table))
+    assert got == want
+
