@@ -166,7 +166,12 @@ typedef struct {
     uint32_t *hist_ring_dev;            /* device, [batch][hist_cap] in/out; may be NULL */
     uint32_t *hist_len_dev;             /* device, [batch] in/out */
     uint32_t hist_cap;
-    uint32_t reserved0;
+    /* Form C: a number the caller changes whenever it writes the ring or
+     * hist_len_dev itself (a new sequence, a new prompt). While it stays the
+     * same and each call finds exactly the one token the library recorded
+     * since the last call, the window counts are updated by that token
+     * instead of counted again. */
+    uint32_t hist_epoch;
     /* Greedy rows with anti_restate (sampling.rs:472-474). The device picks
      * the guard's candidates: guard_out[b][0] = the raw argmax,
      * guard_out[b][1..8] = the ids of the 8 largest finite penalized logits

@@ -108,7 +108,7 @@ class BatchC(ctypes.Structure):
         ("hist_ring_dev", ctypes.c_void_p),
         ("hist_len_dev", ctypes.c_void_p),
         ("hist_cap", ctypes.c_uint32),
-        ("reserved0", ctypes.c_uint32),
+        ("hist_epoch", ctypes.c_uint32),
         ("guard_out", ctypes.c_void_p),
         ("decoder", ctypes.POINTER(TokenBytesC)),
     ]

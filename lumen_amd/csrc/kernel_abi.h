@@ -149,7 +149,13 @@ struct KernelArgs {
   uint32_t* ring_len;
   uint32_t* hist_end;        // [B] end of row b's counts (hist_off[b] = kHistBad on overflow)
   uint32_t ring_cap;
-  uint32_t pad2;
+  uint32_t ring_epoch;       // lumen_batch.hist_epoch
+  // [B][8] what row b's counts reflect: ring_len, window, ring address (lo,
+  // hi), ring_cap, ring_epoch. When the next call finds exactly one more token recorded
+  // in the same ring with the same window, lumen_hist_window updates the
+  // counts by that token (and the one leaving the window) instead of counting
+  // the window again. ring_len 0xffffffff: nothing valid.
+  uint32_t* hist_state;
   // Anti-restate rows: candidates to guard[B][kGuardWords] (device) and, in
   // synchronous calls, to guard_mapped (mapped pinned host memory) before
   // the row is counted in done_mapped.

@@ -153,7 +153,8 @@ struct lumen_sampler {
   DevBuf guard;  // [B][kGuardWords] anti-restate candidates when the caller passes none
   uint32_t* guard_dev = nullptr;  // where the last call's candidates went
   bool any_anti = false;          // the last call had anti-restate rows
-  DevBuf wcnt;  // device history: [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts
+  DevBuf wcnt;  // device history: [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts, [B][8] state
+  size_t wcnt_state_off = 0;  // word offset of the state in wcnt (layout of the last call)
   int cu_count = 0;
   int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
   hipEvent_t staged = nullptr;  // recorded after the last staging copy
@@ -716,9 +717,20 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   }
   if (ring) {
     const size_t cap = bt->hist_cap;
-    int rc = ensure_dev(s->wcnt, sizeof(uint32_t) * (2 * B + 2 * cap * B));
+    // [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts, [kMaxStateRows][8] state
+    const size_t state_off = 2 * B + 2 * cap * B;
+    const size_t need = sizeof(uint32_t) * (state_off + 8 * (size_t)B);
+    const void* before = s->wcnt.p;
+    int rc = ensure_dev(s->wcnt, need);
     if (rc != LUMEN_OK) return rc;
     uint32_t* w = static_cast<uint32_t*>(s->wcnt.p);
+    if (s->wcnt.p != before || s->wcnt_state_off != state_off) {
+      // a new layout: nothing counted yet
+      if (hipMemsetAsync(w + state_off, 0xff, sizeof(uint32_t) * 8 * (size_t)B, st) != hipSuccess)
+        return fail(LUMEN_ERR_HIP, "window-count state init");
+      s->wcnt_state_off = state_off;
+    }
+    ka.hist_state = w + state_off;
     ka.hist_off = w;
     ka.hist_end = w + B;
     ka.hist_ids = w + 2 * B;
@@ -726,6 +738,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     ka.ring = bt->hist_ring_dev;
     ka.ring_len = bt->hist_len_dev;
     ka.ring_cap = bt->hist_cap;
+    ka.ring_epoch = bt->hist_epoch;
   } else if (!host_csr) {
     ka.hist_off = bt->pen_offsets;
     ka.hist_ids = bt->pen_ids;

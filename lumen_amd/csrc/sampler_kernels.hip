@@ -3471,6 +3471,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
   __shared__ uint32_t hkey[kHashSlots];
   __shared__ uint32_t hcnt[kHashSlots];
   __shared__ uint32_t nout;
+  __shared__ uint32_t pout_s;
   const uint32_t b = blockIdx.x, t = threadIdx.x;
   if (b >= a.batch) return;
   const RowParams& P = a.inline_rows ? a.inline_params[b] : a.params[b];
@@ -3481,11 +3482,24 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
   uint32_t* cnt = const_cast<uint32_t*>(a.hist_cnt);
   const uint32_t len = a.ring_len[b];
   const uint32_t w = (P.window > 0u && P.window < len) ? P.window : len;
+  uint32_t* st = a.hist_state + (uint64_t)b * 8u;
+  const uint64_t rid = (uint64_t)(uintptr_t)a.ring;
+  auto set_state = [&](uint32_t l) {
+    if (t == 0) {
+      st[0] = l;
+      st[1] = P.window;
+      st[2] = (uint32_t)rid;
+      st[3] = (uint32_t)(rid >> 32);
+      st[4] = cap;
+      st[5] = a.ring_epoch;
+    }
+  };
   if (!(P.flags & kPen) || w == 0u) {
     if (t == 0) {
       off[b] = base;
       a.hist_end[b] = base;
     }
+    set_state((P.flags & kPen) ? len : 0xffffffffu);
     return;
   }
   if (w > cap) {
@@ -3494,7 +3508,64 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
       off[b] = kHistBad;
       a.hist_end[b] = base;
     }
+    set_state(0xffffffffu);
     return;
+  }
+  const bool follows = st[0] != 0xffffffffu && st[0] + 1u == len && st[1] == P.window &&
+                       st[2] == (uint32_t)rid && st[3] == (uint32_t)(rid >> 32) && st[4] == cap && st[5] == a.ring_epoch &&
+                       off[b] == base;
+  if (follows) {
+    // one token recorded since the counts were made (by the sampler): add
+    // it, and take out the token that left a full window
+    const uint32_t* ring = a.ring + (uint64_t)base;
+    const uint32_t tin = ring[(len - 1u) % cap];
+    const bool leaves = P.window > 0u && len - 1u >= P.window;
+    const uint32_t tout = leaves ? ring[(len - 1u - P.window) % cap] : kHashEmpty;
+    const uint32_t n0 = a.hist_end[b] - base;
+    if (t == 0) {
+      nout = kHashEmpty;   // position of tin
+      pout_s = kHashEmpty;  // position of tout
+    }
+    __syncthreads();
+    if (tin != tout)
+      for (uint32_t j = t; j < n0; j += blockDim.x) {
+        const uint32_t id = ids[base + j];
+        if (id == tin) nout = j;
+        if (leaves && id == tout) pout_s = j;
+      }
+    __syncthreads();
+    const uint32_t pin = nout, pout = pout_s;
+    if (!(tin != tout && leaves && pout == kHashEmpty)) {
+      if (t == 0) {
+        uint32_t n = n0;
+        if (tin != tout) {
+          if (pin != kHashEmpty) {
+            cnt[base + pin] += 1u;
+          } else {
+            ids[base + n] = tin;
+            cnt[base + n] = 1u;
+            ++n;
+          }
+          if (leaves) {
+            const uint32_t c = cnt[base + pout] - 1u;
+            if (c) {
+              cnt[base + pout] = c;
+            } else {
+              // the last entry takes the freed place
+              --n;
+              ids[base + pout] = ids[base + n];
+              cnt[base + pout] = cnt[base + n];
+            }
+          }
+        }
+        off[b] = base;
+        a.hist_end[b] = base + n;
+        st[0] = len;
+      }
+      return;
+    }
+    // the counts do not hold the leaving token: count the window again
+    __syncthreads();
   }
   for (uint32_t i = t; i < kHashSlots; i += blockDim.x) {
     hkey[i] = kHashEmpty;
@@ -3528,5 +3599,6 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
     off[b] = base;
     a.hist_end[b] = base + nout;
   }
+  set_state(len);
 }
 }  // namespace lumen

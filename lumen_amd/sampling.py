@@ -14,6 +14,7 @@ either way). Every call goes through liblumen_sampler.so; there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import itertools
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence
 
@@ -159,7 +160,7 @@ class Engine:
                      rngs: Optional[Sequence[Xorshift64]] = None,
                      penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
                      sync: bool = True, stream=None, uniforms_dev=None, rng_states_dev=None,
-                     hist_ring_dev=None, hist_len_dev=None, guard_out=None, decoder=None):
+                     hist_ring_dev=None, hist_len_dev=None, hist_epoch=0, guard_out=None, decoder=None):
         """Samples every row of `logits` [B, V].
 
         histories: SamplerState.history per row (the window is applied here),
@@ -171,7 +172,10 @@ class Engine:
         from and advanced by the kernel (greedy rows keep their state).
         hist_ring_dev / hist_len_dev: device-resident history (an int32
         [B, cap] ring and an int32 [B] count of recorded tokens); the window
-        is counted on the device and each row's token recorded there.
+        is counted on the device and each row's token recorded there;
+        hist_epoch: changed by the caller whenever it writes the ring itself
+        (between calls that only the library appended to, the counts are
+        updated by the one new token instead of counted again).
         guard_out: an int32 device [B, 9] tensor for the anti-restate
         candidates (required for anti_restate rows when sync=False);
         decoder: TokenBytes (or a list of bytes per id) for the guard's
@@ -219,6 +223,7 @@ class Engine:
             bt.hist_ring_dev = hist_ring_dev.data_ptr()
             bt.hist_len_dev = hist_len_dev.data_ptr()
             bt.hist_cap = hist_ring_dev.shape[1]
+            bt.hist_epoch = int(hist_epoch) & 0xFFFFFFFF
         if guard_out is not None:
             bt.guard_out = guard_out.data_ptr()
         if decoder is not None:
@@ -292,12 +297,22 @@ def anti_restate_select(candidates: Sequence[int], history: Sequence[int],
         c, h.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), h.size, d))
 
 
+_epochs = itertools.count(1)
+
+
+def next_epoch() -> int:
+    """A fresh DeviceDecodeState epoch (see lumen_batch.hist_epoch)."""
+    return next(_epochs)
+
+
 class DeviceDecodeState:
     """Per-row decode state kept in device memory: the Xorshift64 state
     (Sampler::rng, sampling.rs:395-403) and the history ring
     (SamplerState::history, sampling.rs:353-389) of `cap` tokens. A decode
     step samples with `step(engine, logits, params)`: no host draw, no
-    history upload, and the sampled tokens are recorded on the device."""
+    history upload, and the sampled tokens are recorded on the device.
+    Writing `ring` or `lens` directly (a new prompt) must be followed by
+    `self.epoch = next_epoch()`, so the window counts are made again."""
 
     def __init__(self, seeds: Sequence[int], cap: int = 4096, device: int = 0,
                  histories: Optional[Sequence[Sequence[int]]] = None):
@@ -316,10 +331,12 @@ class DeviceDecodeState:
             lens[b] = h.size
         self.ring = torch.from_numpy(ring.view(np.int32)).to(dev)
         self.lens = torch.from_numpy(lens.view(np.int32)).to(dev)
+        self.epoch = next(_epochs)
 
     def step(self, eng: "Engine", logits, params: Sequence[SamplingParams], **kw):
         return eng.sample_batch(logits, params, rng_states_dev=self.rng,
-                                hist_ring_dev=self.ring, hist_len_dev=self.lens, **kw)
+                                hist_ring_dev=self.ring, hist_len_dev=self.lens,
+                                hist_epoch=self.epoch, **kw)
 
 
 class PreparedBatch:

@@ -579,6 +579,46 @@ def test_device_decode_state(eng, V):
     assert [int(v) for v in st] == [r.state() for r in host_rng]
 
 
+def test_device_history_rewrite(eng):
+    # counts updated token by token across calls, then the ring rewritten by
+    # the caller (a new prompt, a new epoch): the counts are made again, and
+    # the following calls update them again
+    import torch
+    from lumen_amd.sampling import DeviceDecodeState, Xorshift64, next_epoch
+
+    V, B = 3000, 4
+    rng = np.random.default_rng(5)
+    params = [SP(temperature=0.0, repetition_penalty=1.5, repeat_last_n=3),
+              SP(temperature=0.8, frequency_penalty=1.0),
+              SP(temperature=0.0, presence_penalty=2.0, repeat_last_n=1),
+              SP(temperature=1.0, top_k=30, repetition_penalty=1.3, repeat_last_n=5)]
+    seeds = [1, 2, 3, 4]
+    ds = DeviceDecodeState(seeds, cap=32, histories=[[1, 2, 3]] * B)
+    hist = [[1, 2, 3] for _ in range(B)]
+    host_rng = [Xorshift64(s) for s in seeds]
+    for phase in range(2):
+        for step in range(6):
+            lg = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+            for b in range(B):
+                lg[b, hist[b][-4:]] += 3.0
+            x = torch.from_numpy(lg).to("cuda:0")
+            log(f"case history rewrite phase {phase} step {step}")
+            _, want = eng.sample_batch(x, params, histories=[np.array(h, np.uint32) for h in hist],
+                                       rngs=host_rng)
+            _, got = ds.step(eng, x, params)
+            assert got == want, (phase, step, got, want)
+            for b in range(B):
+                hist[b].append(want[b])
+        # a new prompt written by the caller
+        prompt = rng.integers(0, V, size=5).astype(np.uint32)
+        ring = np.zeros((B, 32), np.uint32)
+        ring[:, :5] = prompt
+        ds.ring.copy_(torch.from_numpy(ring.view(np.int32)))
+        ds.lens.fill_(5)
+        ds.epoch = next_epoch()
+        hist = [list(prompt) for _ in range(B)]
+
+
 def test_device_history_overflow(eng):
     # a whole-history penalty window longer than the ring cannot be counted:
     # that row reports an error (status 3) and the other rows are unaffected
