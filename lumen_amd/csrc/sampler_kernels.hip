@@ -3343,7 +3343,6 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
     return;
   }
   tr.windows = 1;
-  tr.pad[1] = n;  // diagnostics: candidates in the window
   tr.topp_kept = (uint32_t)wk.pos + 1u;
   tr.topp_cum = wk.c;
   const uint32_t nk = (uint32_t)wk.pos + 1u;
