@@ -24,12 +24,16 @@ SO = os.path.join(LIB, "liblumen_sampler.so")
 
 # Device flags: gfx950 only; every f32 operation stays a single IEEE operation
 # (no contraction into FMA), f32 denormals are kept (as on the x86 host the
-# reference runs on), no packed-FP32 instructions.
+# reference runs on), no packed-FP32 instructions, SGPR spills kept in VGPRs.
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "--offload-device-only", "--no-gpu-bundle-output", "-O3",
     "-std=c++17",
     "-ffp-contract=off", "-fno-gpu-flush-denormals-to-zero", "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # SGPR spills go to VGPR lanes reserved up front, so the lane-holding VGPR
+    # is never itself spilled to scratch (whose reloads wait on every vector
+    # memory load in flight): -3 us on the mixed config-3 batch
+    "-mllvm", "--amdgpu-prealloc-sgpr-spill-vgprs",
 ]
 
 
