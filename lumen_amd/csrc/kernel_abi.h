@@ -61,14 +61,14 @@ enum RowStatus : uint32_t {
 // Device history rings hold at most this many tokens per row (the window
 // counts are built in an LDS hash table of twice as many slots).
 constexpr uint32_t kRingMaxCap = 8192;
-constexpr uint32_t kHistBad = 0xffffffffu;
-constexpr uint32_t kTokenError = 0xffffffffu;  // LUMEN_TOKEN_ERROR  // hist_end value of a row whose window overflowed
+constexpr uint32_t kHistBad = 0xffffffffu;     // hist_off value of a row whose window overflowed
+constexpr uint32_t kTokenError = 0xffffffffu;  // LUMEN_TOKEN_ERROR
 
 constexpr int kInlineRows = 8;
 constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
 constexpr uint32_t kIdleBlock = 0xffffffffu;
-constexpr int kCandCap = 8192;
-constexpr int kMassBins = 512;       // top-p window planning bins      // per-row candidate buffer (entries)
+constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
+constexpr int kMassBins = 512;      // top-p window planning bins
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
 constexpr int kRowRecs = kMaxSlices * kChainMaxQ * 16;  // run records per row (one per wave segment)
 constexpr int kRecWords = 1152;     // words per run record slot
