@@ -2172,14 +2172,22 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   };
   float m3 = kNegInf;
   uint32_t nan3 = 0;
-  row_foreach(row, [&](uint32_t i, float v) {
-    float w = wf(i, v);
-    m3 = rmax(m3, w);
-    nan3 |= is_nan(w) ? 1u : 0u;
-  });
-  m3 = block_rmax(m3, s);
-  nan3 = block_or_u32(nan3, s);
-  tr.passes++;
+  if (pmode == 3 && !mmask && !(P.flags & kMinP) && P.inv_temp == 1.0f &&
+      (tkey(m1) >> 16) > pk_hi) {
+    // The value walk ran on a NaN-free row with a finite maximum m1, and every
+    // element whose value pattern lies above the boundary group is kept: the
+    // kept set holds m1, and x * 1.0f == x, so its maximum is m1.
+    m3 = m1;
+  } else {
+    row_foreach(row, [&](uint32_t i, float v) {
+      float w = wf(i, v);
+      m3 = rmax(m3, w);
+      nan3 |= is_nan(w) ? 1u : 0u;
+    });
+    m3 = block_rmax(m3, s);
+    nan3 = block_or_u32(nan3, s);
+    tr.passes++;
+  }
   LUMEN_TICK("rs_m3", b);
   tr.final_max = m3;
   uint32_t tok;
