@@ -392,6 +392,12 @@ def test_bf16_topp_by_value(eng):
     params.append(SP(temperature=1.3, top_p=0.97, top_k=5000, min_p=0.001))
     rows.append(np.full(V, 1.5))                                  # one value everywhere
     params.append(SP(temperature=1.0, top_p=0.5))
+    # distinct tiny values whose probabilities all round to 1/S1: the boundary
+    # group holds the row maximum (placed last), so only part of it is kept
+    rows.append(np.r_[rng.normal(0, 1, V - 1) * 1e-30, 4e-30])
+    params.append(SP(temperature=1.0, top_p=0.5))
+    rows.append(rng.integers(-4, 5, V) * 0.5)                     # tied maxima kept whole at T = 1
+    params.append(SP(temperature=1.0, top_p=0.9))
     bits = to_bf16_bits(np.array(rows, dtype=np.float32))
     f32 = (bits.astype(np.uint32) << 16).view(np.float32)
     B = len(rows)
