@@ -35,6 +35,10 @@
 
 namespace lumen {
 
+#ifdef LUMEN_EST_STOP
+__device__ int g_est_stop;
+#endif
+
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr uint32_t kSat = 1u << 30;
@@ -329,6 +333,11 @@ struct EstShared {
   uint32_t seg_bin[kEstMaxB + 1];
   PMap seg_tot[kEstMaxB + 1];
   float bx[kEstBx];
+  // ecss_chunk4: per-wave summaries and their exclusive prefixes
+  uint32_t xw[4][kWaves];
+  PMap xm[kWaves];
+  uint32_t pxh[kWaves], pxc[kWaves];
+  PMap pxm[kWaves];
 };
 
 struct SegVal {
@@ -694,6 +703,9 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
   __syncthreads();
   const double p_start = (double)c + pre + inc - d;
   const double rel = (double)((t + 1) * M) * 0x1.0p-24 * 1.01 + 1e-9;
+#ifdef LUMEN_EST_STOP
+  if (g_est_stop == 1) { EcssResult z{c, 0, -1, 0.f}; return z; }
+#endif
 #ifdef LUMEN_TICK_FINAL
   LUMEN_TICK("e_scan", 0);
 #endif
@@ -703,6 +715,9 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
     if (t == 0) es.fail = 2;  // structure did not fit (diagnostic only)
     return ecss_chunk<M>(c, x, mode, theta, sh);
   }
+#ifdef LUMEN_EST_STOP
+  if (g_est_stop == 2) { EcssResult z{c, 0, -1, 0.f}; return z; }
+#endif
 #ifdef LUMEN_TICK_FINAL
   LUMEN_TICK("e_prep", 0);
 #endif
@@ -713,6 +728,238 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
     return r;
   }
   return ecss_chunk<M>(c, x, mode, theta, sh);
+}
+
+// ---------------------------------------------------------------------------
+// The estimate-guided method for one chunk of at most 4 * kThreads summands
+// (thread t holds x[4] = chunk elements 4t .. 4t+3, zero past the end; the
+// first nact threads hold any), from the exact running sum c. Same method as
+// ecss_fast_chunk, with each cross-wave step (the f64 prefix, the segmented
+// composition of runs, the boundary ordinals) done once by wave 0 instead
+// of by every thread, and the runs, boundaries and their summands gathered
+// so that the walk on wave 0 reads them from its registers. The drift bound
+// is rigorous (each add rounds by at most 2^-24 of the running sum, which
+// never decreases), so the estimate only decides which threads are replayed;
+// a walk check that fails anyway falls back to ecss_chunk.
+__device__ __forceinline__ double dadd(double l, double r) { return l + r; }
+
+__device__ __forceinline__ EcssResult ecss_chunk4(float c, const float (&x)[4], int mode,
+                                                  float theta, int nact, EcssShared& sh,
+                                                  EstShared& es) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const bool act = t < nact;
+  // 1. f64 estimate of the running sum at each thread's start
+  const double d = ((double)x[0] + (double)x[1]) + ((double)x[2] + (double)x[3]);
+  const double winc = wave_scan_incl(d, 0.0, dadd);
+  double* dw = reinterpret_cast<double*>(sh.wave_tot);
+  double* dp = reinterpret_cast<double*>(sh.wave_pre);
+  if (lane == 63) dw[w] = winc;
+  __syncthreads();
+  if (w == 0) {
+    const double v = lane < kWaves ? dw[lane] : 0.0;
+    const double vi = wave_scan_incl(v, 0.0, dadd);
+    if (lane < kWaves) dp[lane] = vi - v;
+  }
+  __syncthreads();
+  const double P = (double)c + dp[w] + (winc - d);
+#ifdef LUMEN_EST_STOP
+  if (g_est_stop == 11) { EcssResult z{c, 0, -1, 0.f}; return z; }
+#endif
+
+  const double rel = (double)(4 * t + 4) * 0x1.0p-24 * 1.001 + 1e-12;
+  const uint32_t lo = est_binade(P * (1.0 - rel));
+  const uint32_t hi = est_binade((P + d) * (1.0 + rel));
+  const bool bnd = act && lo != hi;
+  PMap m{0u, 0u};
+  if (act && !bnd) {
+    float y0 = __uint_as_float(lo), y1 = __uint_as_float(lo | 1u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      y0 = __fadd_rn(y0, x[j]);
+      y1 = __fadd_rn(y1, x[j]);
+    }
+    const uint32_t n0 = __float_as_uint(y0) - lo, n1 = __float_as_uint(y1) - (lo | 1u);
+    m.a0 = n0 > kSat ? kSat : n0;
+    m.a1 = n1 > kSat ? kSat : n1;
+  }
+  // 2. runs of certain threads between boundary threads
+  const SegVal id{0u, PMap{0u, 0u}};
+  const SegVal inc = wave_scan_incl(SegVal{bnd ? 1u : 0u, m}, id, seg_combine);
+  const unsigned long long bm = __ballot(bnd);
+  if (lane == 63) {
+    es.xw[0][w] = inc.head;
+    es.xm[w] = inc.m;
+    es.xw[1][w] = (uint32_t)__popcll(bm);
+    es.xw[2][w] = bnd ? 1u : 0u;
+    es.xw[3][w] = lo;
+  }
+  __syncthreads();
+  if (w == 0) {
+    const SegVal v = lane < kWaves ? SegVal{es.xw[0][lane], es.xm[lane]} : id;
+    const SegVal ex = wave_shr1(wave_scan_incl(v, id, seg_combine), id);
+    const uint32_t cn = lane < kWaves ? es.xw[1][lane] : 0u;
+    const uint32_t ci = wave_scan_incl(cn, 0u, [](uint32_t l, uint32_t r) { return l + r; });
+    if (lane < kWaves) {
+      es.pxh[lane] = ex.head;
+      es.pxm[lane] = ex.m;
+      es.pxc[lane] = ci - cn;
+    }
+    if (lane == kWaves - 1) es.nb = (int)ci;
+  }
+  __syncthreads();
+  const SegVal ex = seg_combine(SegVal{es.pxh[w], es.pxm[w]}, wave_shr1(inc, id));
+  const uint32_t bidx = es.pxc[w] + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull));
+  const int nb = es.nb;
+#ifdef LUMEN_EST_STOP
+  if (g_est_stop == 12) { EcssResult z{c, 0, -1, 0.f}; return z; }
+#endif
+
+  if (nb > 63) {
+    __syncthreads();
+    return ecss_chunk<4>(c, x, mode, theta, sh);
+  }
+  uint32_t pb = wave_shr1(bnd ? 1u : 0u, 1u), plo = wave_shr1(lo, 0u);
+  if (lane == 0) {
+    pb = w > 0 ? es.xw[2][w - 1] : 1u;
+    plo = w > 0 ? es.xw[3][w - 1] : 0u;
+  }
+  if (bnd) {
+    es.seg_bin[bidx] = pb ? kEmptyRun : plo;
+    es.seg_tot[bidx] = pb ? PMap{0u, 0u} : ex.m;
+    es.bpos[bidx] = (uint16_t)t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) es.bx[4u * bidx + (uint32_t)j] = x[j];
+  }
+  if (t == nact - 1) {
+    es.seg_bin[nb] = bnd ? kEmptyRun : lo;
+    es.seg_tot[nb] = bnd ? PMap{0u, 0u} : seg_combine(ex, SegVal{0u, m}).m;
+  }
+  __syncthreads();
+#ifdef LUMEN_EST_STOP
+  if (g_est_stop == 13) { EcssResult z{c, 0, -1, 0.f}; return z; }
+#endif
+
+  // 3. the walk over runs and boundaries, on wave 0 (uniform values)
+  if (w == 0) {
+    uint32_t sb_r = kEmptyRun, a0_r = 0, a1_r = 0, bp_r = 0;
+    float bx_r[4] = {0.f, 0.f, 0.f, 0.f};
+    if (lane <= nb) {
+      sb_r = es.seg_bin[lane];
+      a0_r = es.seg_tot[lane].a0;
+      a1_r = es.seg_tot[lane].a1;
+    }
+    if (lane < nb) {
+      bp_r = es.bpos[lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bx_r[j] = es.bx[4 * lane + j];
+    }
+    uint32_t cb = __float_as_uint(c);
+    int fail = 0, hit_seg = -1, hit_pos = -1;
+    uint32_t cseg = 0, bef = 0;
+    for (int k = 0; k <= nb; ++k) {
+      const uint32_t sb = (uint32_t)__builtin_amdgcn_readlane((int)sb_r, k);
+      if (sb != kEmptyRun) {
+        const uint32_t m0 = (uint32_t)__builtin_amdgcn_readlane((int)a0_r, k);
+        const uint32_t m1 = (uint32_t)__builtin_amdgcn_readlane((int)a1_r, k);
+        const uint32_t ic = (cb & 1u) ? m1 : m0;
+        const uint32_t nbits = cb + ic;
+        if ((cb & 0xff800000u) != sb || ic >= kSat || nbits >= sb + 0x00800000u) {
+          fail = 1;
+          break;
+        }
+        if (mode != kEcssSum && ecss_cond(mode, __uint_as_float(nbits), theta)) {
+          hit_seg = k;
+          cseg = cb;
+          break;
+        }
+        cb = nbits;
+      }
+      if (k == nb) break;
+      // the boundary thread's summands, with the running sum kept uniform
+      // (scalar registers) between the adds
+      float ys[4];
+      float y = __uint_as_float(cb);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xq = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bx_r[q]), k));
+        y = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__fadd_rn(y, xq))));
+        ys[q] = y;
+      }
+      int j = 4;
+      if (mode != kEcssSum) {
+#pragma unroll
+        for (int q = 3; q >= 0; --q) j = ecss_cond(mode, ys[q], theta) ? q : j;
+      }
+      if (j < 4) {
+        hit_pos = 4 * __builtin_amdgcn_readlane((int)bp_r, k) + j;
+        bef = j ? __float_as_uint(ys[j > 0 ? j - 1 : 0]) : cb;
+        cb = __float_as_uint(ys[j]);
+        break;
+      }
+      cb = __float_as_uint(y);
+    }
+    if (lane == 0) {
+      es.fail = fail;
+      es.hit_seg = hit_seg;
+      es.hit_pos = hit_pos;
+      es.c_out = __uint_as_float(cb);
+      es.c_seg = __uint_as_float(cseg);
+      es.before = __uint_as_float(bef);
+    }
+  }
+  __syncthreads();
+  EcssResult r;
+  r.c = es.c_out;
+  r.before = es.before;
+  r.found = es.hit_pos >= 0 ? 1 : 0;
+  r.pos = es.hit_pos;
+  const int fail = es.fail, hit_seg = es.hit_seg;
+  __syncthreads();
+  if (fail) return ecss_chunk<4>(c, x, mode, theta, sh);
+  if (hit_seg < 0) return r;
+  // 4. the hit is inside run hit_seg: exact starts of its threads, then the
+  // first thread whose end meets the condition replays its summands
+  {
+    const uint32_t cs = __float_as_uint(r.c);  // c_out holds the run start here
+    const uint32_t c0 = __float_as_uint(es.c_seg);
+    (void)cs;
+    const bool in = act && !bnd && bidx == (uint32_t)hit_seg;
+    uint32_t sbits = 0, ebits = 0;
+    if (in) {
+      const uint32_t bfr = (c0 & 1u) ? ex.m.a1 : ex.m.a0;
+      sbits = c0 + bfr;
+      ebits = sbits + (((c0 ^ bfr) & 1u) ? m.a1 : m.a0);
+    }
+    const bool h = in && ecss_cond(mode, __uint_as_float(ebits), theta);
+    const unsigned long long hm = __ballot(h);
+    if (lane == 0) sh.red_h[w] = hm ? (w * 64 + __ffsll((long long)hm) - 1) : kThreads;
+    __syncthreads();
+    int th = kThreads;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) th = min(th, sh.red_h[i]);
+    if (t == th) {
+      float y = __uint_as_float(sbits), p = y;
+      int j = 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (j == 4) {
+          p = y;
+          y = __fadd_rn(y, x[q]);
+          if (ecss_cond(mode, y, theta)) j = q;
+        }
+      }
+      es.hit_pos = 4 * th + j;
+      es.c_out = y;
+      es.before = p;
+    }
+    __syncthreads();
+    r.found = 1;
+    r.pos = es.hit_pos;
+    r.c = es.c_out;
+    r.before = es.before;
+    __syncthreads();
+    return r;
+  }
 }
 
 }  // namespace lumen

@@ -68,4 +68,32 @@ __device__ __forceinline__ float expf_glibc(float x) {
   return __double2float_rn(y);
 }
 
+// expf_glibc for x <= 0 or x = -inf (NaN excluded), without branches: the
+// special cases of the general routine reduce to one, x < -0x1.9fe368p6f
+// (the result underflows to 0, as for -inf), decided by a select after the
+// ordinary computation on a clamped argument. Bit-identical to expf_glibc on
+// that domain.
+__device__ __forceinline__ float expf_glibc_nonpos(float x) {
+  const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+  const double C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  const double C2 = 0x1.62e42ff0c52d6p-1 / 32;
+  const double SHIFT = 0x1.8p+52;
+  const double INVLN2N = 0x1.71547652b82fep+0 * 32;
+  const float xc = fmaxf(x, -0x1.ap6f);  // -104: inside the table's range
+  const double xd = (double)xc;
+  double kd = __fma_rn(INVLN2N, xd, SHIFT);
+  const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd = __dsub_rn(kd, SHIFT);
+  const double r = __fma_rn(INVLN2N, xd, -kd);
+  const uint64_t t = g_exp2_lds[ki & 31] + (ki << 47);
+  const double sc = __longlong_as_double((long long)t);
+  const double z = __fma_rn(C0, r, C1);
+  const double r2 = __dmul_rn(r, r);
+  double y = __fma_rn(C2, r, 1.0);
+  y = __fma_rn(z, r2, y);
+  y = __dmul_rn(y, sc);
+  const float f = __double2float_rn(y);
+  return x < -0x1.9fe368p6f ? 0.0f : f;
+}
+
 }  // namespace lumen

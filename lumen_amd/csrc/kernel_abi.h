@@ -68,6 +68,9 @@ constexpr int kInlineRows = 8;
 constexpr int kMaxSlices = 16;      // workgroups cooperating on one row
 constexpr uint32_t kIdleBlock = 0xffffffffu;
 constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
+// Row stride of the candidate buffers: kCandCap entries, then (register-
+// resident top-p rows) each candidate's exp(v - m1) as a u32 array.
+constexpr int kCandStride = 2 * kCandCap;
 constexpr int kMassBins = 512;      // top-p window planning bins
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
 constexpr int kRowRecs = kMaxSlices * kChainMaxQ * 16;  // run records per row (one per wave segment)
@@ -88,6 +91,12 @@ struct RowWs {
   uint64_t part_arg[kMaxSlices];
   double part_e[kMaxSlices];
   uint64_t part_top[kMaxSlices][8];  // anti-restate rows: each slice's 8 largest finite keys
+  // register-resident top-p rows: each slice's candidate block (start, count)
+  // in the row's candidate buffer and its exact-sum record (items, raw slots)
+  uint32_t part_cb[kMaxSlices];
+  uint32_t part_cn[kMaxSlices];
+  uint32_t part_nrec[kMaxSlices];
+  uint32_t part_nraw[kMaxSlices];
 };
 
 // Anti-restate candidates per row: [0] the raw argmax (total_cmp over every

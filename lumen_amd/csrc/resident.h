@@ -1,0 +1,807 @@
+// Register-resident split path for top-p rows (included by sampler_kernels.hip).
+//
+// Reference semantics: apply_top_p_on_logits (crates/lumen-runtime/src/
+// sampling.rs:942-967) after the penalties (:850-900) and before min-p,
+// temperature, softmax and the draw (:510-526, :207-231, :1003-1014).
+//
+// Each of the G workgroups of a row owns a slice of at most kResSlice logits
+// and reads it from HBM exactly once: thread t keeps slice elements
+// 32t .. 32t+31 in registers (contiguous, so a thread's part of any
+// sequential sum is one run of adds). The loads are coalesced; an LDS
+// transpose hands each thread its own run. Then:
+//
+//  phase A  penalties (patched in the LDS copy), the slice maximum, an
+//           exp-sum estimate, and the candidates: every logit at or above a
+//           threshold sampled from the row (the same in every slice), written
+//           in index order to the row's candidate buffer;
+//  barrier  the row maximum m1 and each slice's exp-sum estimate;
+//  phase B  the exact summands exp(v - m1) and the slice's record of the
+//           exact sequential f32 softmax sum (runs of whole threads as parity
+//           maps of ecss.h, plus the raw summands of the few threads whose
+//           binade the estimate cannot fix);
+//  finisher the last workgroup to arrive walks the G records in order (the
+//           exact S1), takes the candidates in index order, sorts the window
+//           that holds the nucleus by (p desc, id asc), walks the exact
+//           cumulative sum to the crossing, keeps the nucleus in index order
+//           and runs the final stage (min-p, temperature, softmax, draw).
+//
+// Every estimate only decides speed: a record run is applied only after
+// checking that the exact running sum sits inside its binade and stays
+// there, and any check that fails, a candidate set that misses the
+// crossing, or a timeout hands the row to the exact single-workgroup path.
+#pragma once
+
+namespace lumen {
+
+constexpr uint32_t kResK = 32;                                    // logits per thread
+constexpr uint32_t kResSlice = kResK * (uint32_t)kThreads;        // logits per slice
+constexpr uint32_t kResPitch = kResK + 4u;                        // LDS words per thread
+constexpr uint32_t kResCandTarget = 5000;                         // candidates aimed at per row
+constexpr uint32_t kResItemCap = 4096;                            // record items per slice
+constexpr uint32_t kResRawOff = 4u * kResItemCap;                 // word offset of the raw area
+constexpr uint32_t kResSliceWords = 32u * (uint32_t)kRecWords;    // record words per slice
+constexpr uint32_t kResRawCap = (kResSliceWords - kResRawOff) / kResK;  // uncertain threads per slice
+constexpr uint32_t kNoRaw = 0xffffffffu;
+constexpr uint32_t kResWindowCap = (uint32_t)kCap / 2u;          // sorted in place with its own spare half
+static_assert((uint32_t)kMaxSlices * 32u <= (uint32_t)kRowRecs, "slice record areas fit the row");
+
+// Development aid: -DLUMEN_RES_STOP=k makes the rows of this path stop after
+// phase k (wrong tokens), so that the kernel time of each prefix of the
+// critical path can be measured. Never defined in the shipped build.
+#ifdef LUMEN_RES_STOP
+#define RES_STOP(k)                             \
+  do {                                          \
+    if (LUMEN_RES_STOP == (k)) {                \
+      if (threadIdx.x == 0) a.tokens[b] = 0u;   \
+      return;                                   \
+    }                                           \
+  } while (0)
+#else
+#define RES_STOP(k) do { } while (0)
+#endif
+
+__device__ __forceinline__ float* res_buf(Smem& s) { return reinterpret_cast<float*>(s.A); }
+
+__device__ __forceinline__ uint32_t* res_rec(const KernelArgs& a, int b, uint32_t sl) {
+  return a.est + ((uint64_t)b * kRowRecs + (uint64_t)sl * 32u) * kRecWords;
+}
+
+
+// Issues the coalesced loads of this thread's share of its wave's block:
+// wave w covers slice elements [2048 w, 2048 (w + 1)), lane l loads elements
+// 256 q + 4 l .. +3 of it. The row must be vector aligned (Row::vec) and
+// hold at least 8 logits. Addresses are clamped into the row and elements at
+// or past sc.hi read as -inf, with no branch; when the row length is not a
+// multiple of 4 the partial group at its end is not loaded here (res_tail
+// patches it in the LDS copy).
+template <bool BF16>
+__device__ __forceinline__ void res_issue(const Row& row, Slice sc, float (&v)[8][4]) {
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t base = sc.lo + w * (64u * kResK) + 4u * lane;
+  const uint32_t last4 = (row.V - 4u) & ~3u;  // start of the last whole group of 4
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint32_t i = base + 256u * (uint32_t)q;
+    const uint32_t ic = min(i, last4);
+    float f[4];
+    if (BF16) {
+      const ushort4 h = *reinterpret_cast<const ushort4*>(row.h + ic);
+      f[0] = __uint_as_float((uint32_t)h.x << 16);
+      f[1] = __uint_as_float((uint32_t)h.y << 16);
+      f[2] = __uint_as_float((uint32_t)h.z << 16);
+      f[3] = __uint_as_float((uint32_t)h.w << 16);
+    } else {
+      const float4 g = *reinterpret_cast<const float4*>(row.f + ic);
+      f[0] = g.x;
+      f[1] = g.y;
+      f[2] = g.z;
+      f[3] = g.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[q][j] = (i == ic && i + (uint32_t)j < sc.hi) ? f[j] : kNegInf;
+  }
+}
+
+// The partial group at the end of a row whose length is not a multiple of
+// 4, into the LDS copy of the slice that holds it.
+__device__ __forceinline__ bool res_has_tail(const Row& row, Slice sc) {
+  return (row.V & 3u) != 0u && sc.hi == row.V && sc.hi > sc.lo;
+}
+
+// LDS word of slice element o in the transposed copy.
+__device__ __forceinline__ uint32_t res_slot(uint32_t o) { return (o >> 5) * kResPitch + (o & 31u); }
+
+__device__ __forceinline__ void res_tail(const Row& row, Slice sc, float* L) {
+  const uint32_t t0 = max(sc.lo, row.V & ~3u);
+  if (threadIdx.x < sc.hi - t0) L[res_slot(t0 + threadIdx.x - sc.lo)] = row.at(t0 + threadIdx.x);
+}
+
+// Moves the loaded block through LDS so that thread t holds slice elements
+// 32t .. 32t+31 in x[]. With `patched`, patch(L) runs on the whole LDS copy
+// (all waves) between the store and the read-back. The LDS copy stays valid
+// until the caller writes LDS again. Starts and ends with a barrier.
+template <class Patch>
+__device__ __forceinline__ void res_transpose(const float (&v)[8][4], float (&x)[kResK], Smem& s,
+                                              bool patched, Patch&& patch) {
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
+  float* L = res_buf(s);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const uint32_t e = 256u * (uint32_t)q + 4u * lane;  // element in the wave's block
+    const uint32_t owner = w * 64u + (e >> 5);
+    *reinterpret_cast<float4*>(L + owner * kResPitch + (e & 31u)) =
+        make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+  }
+  __syncthreads();
+  if (patched) {
+    patch(L);
+    __syncthreads();
+  }
+  // pitch 36 words: 16 consecutive lanes read 16 distinct 4-bank groups
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float4 f = *reinterpret_cast<const float4*>(L + t * kResPitch + 4u * (uint32_t)m);
+    x[4 * m] = f.x;
+    x[4 * m + 1] = f.y;
+    x[4 * m + 2] = f.z;
+    x[4 * m + 3] = f.w;
+  }
+}
+
+__device__ __forceinline__ float block_maxl(float v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_reduce(v, kNegInf, op_maxl);
+  if (lane == 0) s.red_f[w] = v;
+  __syncthreads();
+  float r = kNegInf;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r = op_maxl(r, s.red_f[i]);
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ double block_sum_f64(double v, Smem& s) {
+  double tot;
+  (void)block_excl_scan_f64(v, s, &tot);
+  return tot;
+}
+
+// Exclusive block scan of a u32 with the total (uniform).
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, Smem& s, uint32_t* total) {
+  const uint32_t inc = block_incl_scan_u32(v, s);
+  if (threadIdx.x == kThreads - 1) s.misc_u[0] = inc;
+  __syncthreads();
+  *total = s.misc_u[0];
+  __syncthreads();
+  return inc - v;
+}
+
+struct RecCount {
+  uint32_t items, raws;
+  bool ok;
+};
+
+// Record of the exact sequential f32 sum of this slice's summands (thread t
+// reads its slice elements 32t .. 32t+31 at et, in LDS; nthr threads hold
+// any), entered
+// with a running sum of about p_slice (f64). Thread t's running sum starts
+// near P_t = p_slice + (sum of the summands before it); its binade is
+// certain unless P_t widened by `rel` (the f32 sum drifts from its f64
+// estimate as summands are rounded onto its grid, by up to ~4e-9 per
+// element in logit rows) touches another binade. Items (4 words each):
+//   {bin, a0, a1, kNoRaw}  a run of consecutive certain threads in binade
+//                          bin: grid steps added for an even / odd start;
+//   {bin, a0, a1, r}       one uncertain thread: its map inside bin (used
+//                          when the exact sum is inside bin at its start and
+//                          stays there), else its 32 summands at raw slot r.
+// Items start at rec[0]; raw slot r at rec[kResRawOff + 32 r].
+__device__ __forceinline__ RecCount res_record(const float* et, double p_slice, uint32_t pos0,
+                                               uint32_t nthr, uint32_t* rec, Smem& s) {
+  const uint32_t t = threadIdx.x;
+  const bool live = t < nthr;
+  const float4* e4 = reinterpret_cast<const float4*>(et);  // this thread's 32 summands (LDS)
+  double d = 0.0;
+#pragma unroll
+  for (int m = 0; m < (int)kResK / 4; ++m) {
+    const float4 f = e4[m];
+    d += (double)f.x;
+    d += (double)f.y;
+    d += (double)f.z;
+    d += (double)f.w;
+  }
+  double tot;
+  const double P = p_slice + block_excl_scan_f64(d, s, &tot);
+#ifdef LUMEN_TIMING
+  LUMEN_TICK("rr_scan", 0);
+#endif
+  const double rel = 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
+  const uint32_t blo = est_binade(P * (1.0 - rel));
+  const uint32_t bhi = est_binade((P + d) * (1.0 + rel));
+  const bool unc = live && blo != bhi;
+  const uint32_t bin = unc ? est_binade(P + 0.5 * d) : blo;
+  float y0 = __uint_as_float(bin), y1 = __uint_as_float(bin | 1u);
+#pragma unroll
+  for (int m = 0; m < (int)kResK / 4; ++m) {
+    const float4 f = e4[m];
+    y0 = __fadd_rn(y0, f.x);
+    y1 = __fadd_rn(y1, f.x);
+    y0 = __fadd_rn(y0, f.y);
+    y1 = __fadd_rn(y1, f.y);
+    y0 = __fadd_rn(y0, f.z);
+    y1 = __fadd_rn(y1, f.z);
+    y0 = __fadd_rn(y0, f.w);
+    y1 = __fadd_rn(y1, f.w);
+  }
+  const uint32_t n0 = __float_as_uint(y0) - bin, n1 = __float_as_uint(y1) - (bin | 1u);
+  const PMap own{n0 > kSat ? kSat : n0, n1 > kSat ? kSat : n1};
+  // neighbours' classes: a binade (low 23 bits zero), uncertain or absent
+  constexpr uint32_t kUnc = 1u, kDead = 2u;
+  uint32_t* cls = s.H0;
+  const uint32_t code = !live ? kDead : unc ? kUnc : bin;
+  cls[t] = code;
+  __syncthreads();
+  const uint32_t prv = t > 0 ? cls[t - 1] : kDead;
+  const uint32_t nxt = t + 1 < (uint32_t)kThreads ? cls[t + 1] : kDead;
+  // a run starts after anything else (certain threads never change binade
+  // without an uncertain thread between them) and ends before anything else
+  const bool head = live && (unc || prv != code);
+  const bool last = live && !unc && nxt != code;
+#ifdef LUMEN_TIMING
+  LUMEN_TICK("rr_maps", 0);
+#endif
+  SegVal prev;
+  const SegVal inc = seg_scan_incl(SegVal{head ? 1u : 0u, (live && !unc) ? own : PMap{0u, 0u}},
+                                   s.ecss, s.est, &prev);
+  const uint32_t packed = ((unc || last) ? 1u : 0u) | ((unc ? 1u : 0u) << 16);
+  uint32_t ptot;
+  const uint32_t pos = block_excl_scan_u32(packed, s, &ptot);
+  RecCount rc{ptot & 0xffffu, ptot >> 16, true};
+#ifdef LUMEN_TIMING
+  LUMEN_TICK("rr_scans", 0);
+#endif
+  if (rc.items > kResItemCap || rc.raws > kResRawCap) {
+    rc.ok = false;
+    return rc;
+  }
+  const uint32_t ip = pos & 0xffffu, rp = pos >> 16;
+  if (unc) {
+    *reinterpret_cast<uint4*>(rec + 4u * ip) = make_uint4(bin, own.a0, own.a1, rp);
+    uint4* raw = reinterpret_cast<uint4*>(rec + kResRawOff + kResK * rp);
+    const uint4* u4 = reinterpret_cast<const uint4*>(et);
+#pragma unroll
+    for (int m = 0; m < (int)kResK / 4; ++m) raw[m] = u4[m];
+  } else if (last) {
+    *reinterpret_cast<uint4*>(rec + 4u * ip) = make_uint4(bin, inc.m.a0, inc.m.a1, kNoRaw);
+  }
+  return rc;
+}
+
+// Mass bins of the window planner, on the bits of e = exp(v - m1) in (0, 1]:
+// bin 0 holds the largest values; the shift makes [e_lo, 1] span at most
+// kMassBins bins (e_lo: the smallest candidate value, 0 for all values).
+__device__ __forceinline__ uint32_t res_bin_shift(float e_lo) {
+  const uint32_t span = 0x3f800000u - (__float_as_uint(e_lo) & 0x7fffffffu);
+  uint32_t sh = 0;
+  while ((span >> sh) >= (uint32_t)kMassBins) ++sh;
+  return sh;
+}
+__device__ __forceinline__ uint32_t res_bin(float e, uint32_t sh) {
+  const uint32_t d = 0x3f800000u - min(__float_as_uint(e), 0x3f800000u);
+  return min((uint32_t)kMassBins - 1u, d >> sh);
+}
+// Lower edge of bin h (values of bin h are >= it).
+__device__ __forceinline__ float res_bin_lo(uint32_t h, uint32_t sh) {
+  const uint64_t d = ((uint64_t)(h + 1u) << sh) - 1u;
+  return d >= 0x3f800000ull ? 0.f : __uint_as_float(0x3f800000u - (uint32_t)d);
+}
+
+// Sampled key threshold (the rule of sample_threshold): the sample loads
+// are issued first (res_sample_issue), the slice loads after them, and the
+// selection (res_sample_select) then waits only for the sample.
+__device__ __forceinline__ void res_sample_issue(const Row& row, float (&smp)[4]) {
+  const uint32_t V = row.V;
+  constexpr uint32_t kRuns = kSampleN / 32u;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t j = threadIdx.x + (uint32_t)q * kThreads;
+    const uint32_t c = j >> 5;
+    const uint32_t base = V > kSampleN ? (uint32_t)(((uint64_t)c * (V - 32u)) / (kRuns - 1u)) & ~31u : 0u;
+    smp[q] = V > kSampleN ? row.at(base + (j & 31u)) : 0.f;
+  }
+}
+
+__device__ __forceinline__ uint32_t res_sample_select(const float (&smp)[4], uint32_t V,
+                                                      uint32_t target, Smem& s) {
+  if (V <= kSampleN || target >= V) return 0u;
+  const uint32_t r = (uint32_t)(((uint64_t)target * kSampleN + V - 1) / V);
+  if (r == 0u || r > kSampleN) return 0u;
+  uint32_t* keys = reinterpret_cast<uint32_t*>(s.A);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) keys[threadIdx.x + (uint32_t)q * kThreads] = tkey(smp[q]);
+  __syncthreads();
+  // two digit levels: the lower edge of the bucket holding the r-th key
+  const uint32_t tau = select_desc(kSampleN, [&](uint32_t j) { return keys[j]; }, r - 1u, s, 2);
+  __syncthreads();
+  return tau;
+}
+
+// Top-p (no top-k) over a register-resident slice; see the header comment.
+template <bool BF16>
+__device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
+                                         Smem& s) {
+  ROW_CONTEXT(a, b);
+  const uint32_t V = a.vocab, t = threadIdx.x, lane = t & 63u;
+  const Slice sc = slice_bounds(V, G, sl);
+  const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
+  LUMEN_TICK("r_start", b);
+
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 10) {
+    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+    return;
+  }
+#endif
+  // ---- phase A ----
+  float smp[4];
+  res_sample_issue(row, smp);
+  float v[8][4];
+  res_issue<BF16>(row, sc, v);
+  const uint32_t tau = res_sample_select(smp, V, kResCandTarget, s);
+  const float tv = tau ? key2f(tau) : kNegInf;
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 11) {
+    float acc = 0.f;
+    for (int q = 0; q < 8; ++q) acc += v[q][0] + v[q][1] + v[q][2] + v[q][3];
+    if (acc == 1234.5f && tv == 3.f) a.tokens[b] = 7u;
+    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+    return;
+  }
+#endif
+  float x[kResK];
+  const bool tail = res_has_tail(row, sc);
+  res_transpose(v, x, s, pen || tail, [&](float* L) {
+    if (tail) {
+      res_tail(row, sc, L);
+      if (pen) __syncthreads();
+    }
+    if (!pen) return;
+    // sampling.rs:881-900 on the slice's history ids (each id once)
+    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
+    for (uint32_t j = h0 + t; j < h1; j += kThreads) {
+      const uint32_t id = a.hist_ids[j];
+      if (id >= sc.lo && id < sc.hi) {
+        float& y = L[res_slot(id - sc.lo)];
+        y = penalize(y, a.hist_cnt[j], P);
+      }
+    }
+  });
+  LUMEN_TICK("r_loaded", b);
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 12) {
+    float acc = 0.f;
+    for (int q = 0; q < (int)kResK; ++q) acc += x[q];
+    if (acc == 1234.5f) a.tokens[b] = 7u;
+    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+    return;
+  }
+#endif
+  if (a.pen_out) {
+    float* po = a.pen_out + (uint64_t)b * V + sc.lo + t * kResK;
+#pragma unroll
+    for (int k = 0; k < (int)kResK; ++k)
+      if (sc.lo + t * kResK + (uint32_t)k < sc.hi) po[k] = x[k];
+  }
+  float mt = kNegInf;
+  uint32_t cmask = 0;
+#pragma unroll
+  for (int k = 0; k < (int)kResK; ++k) {
+    mt = op_maxl(mt, x[k]);
+    cmask |= (x[k] >= tv ? 1u : 0u) << k;  // NaN never qualifies
+  }
+  uint32_t ctot;
+  uint32_t coff = block_excl_scan_u32((uint32_t)__popc(cmask), s, &ctot);
+  const float ms = block_maxl(mt, s);
+  float et = 0.f;  // NaN in the slice makes the estimate NaN
+  if (ms != kNegInf) {
+#pragma unroll
+    for (int k = 0; k < (int)kResK; ++k) et += __expf(x[k] - ms);
+  }
+  const double es = block_sum_f64((double)et, s);
+  if (t == 0) {
+    ws.part_max[sl] = ms;
+    ws.part_e[sl] = es;
+    ws.part_cn[sl] = ctot;
+  }
+  LUMEN_TICK("r_phaseA", b);
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 13) {
+    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+    return;
+  }
+#endif
+  wg_arrive(&ws.bar, 0xffffffffu, s);
+  const bool ok = wg_wait_geq(&ws.bar, G, s);
+  if (!ok && t == 0) __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  LUMEN_TICK("r_barrier", b);
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 1) {
+    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+    return;
+  }
+#endif
+
+  // ---- phase B ----
+  // the row's values, one slice per lane of wave 0, in one round trip
+  float* rowv = reinterpret_cast<float*>(s.H0 + 1024);  // [0] m1, [2..3] p_slice (f64)
+  uint32_t* rowu = s.H0 + 1032;                        // [0] ncand, [1] bad, [2] candidate base
+  if (t < 64u) {
+    const bool in = lane < G;
+    const float mi = in ? ws.part_max[lane] : kNegInf;
+    const double ei = in ? ws.part_e[lane] : 0.0;
+    const uint32_t ci = in ? ws.part_cn[lane] : 0u;
+    const float m1w = wave_reduce(mi, kNegInf, op_maxl);
+    const double term = (lane < sl && mi != kNegInf) ? ei * exp((double)mi - (double)m1w) : 0.0;
+    const double ps = wave_reduce(term, 0.0, [](double l, double r) { return l + r; });
+    const uint32_t cin = wave_scan_incl(ci, 0u, op_add_u32);
+    const uint32_t nc = wave_read(cin, 63);
+    const bool nan = __ballot(in && !(ei == ei)) != 0ull;
+    if (lane == sl) rowu[2] = cin - ci;
+    if (lane == 0) {
+      rowv[0] = m1w;
+      *reinterpret_cast<double*>(rowv + 2) = ps;
+      rowu[0] = nc;
+      rowu[1] = (nan || !is_finite(m1w) || nc > (uint32_t)kCandCap) ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+  const float m1 = rowv[0];
+  const double p_slice = *reinterpret_cast<const double*>(rowv + 2);
+  const uint32_t ncand = rowu[0];
+  const uint32_t cbase = rowu[2];
+  bool bad = !ok || rowu[1] != 0u;
+  float* hg = a.hist + ((uint64_t)b * kMaxSlices + sl) * kMassBins;
+  constexpr uint32_t kBins = (uint32_t)kMassBins;
+  if (!bad) {
+    // Candidates in index order at the slice's block: (logit bits << 32) |
+    // id, and exp(v - m1) in the second half of the buffer; their exp-mass
+    // binned by the bits of exp(v - m1) into this slice's histogram (bin 0
+    // holds the largest values). The LDS copy of the slice is indexed by
+    // the bits of cmask: first the logits, then the summands.
+    float* L = res_buf(s);
+    float* hl = reinterpret_cast<float*>(s.H0 + 1536);  // [kBins]
+    float* Lt = L + t * kResPitch;
+    uint32_t* cande = reinterpret_cast<uint32_t*>(cand + kCandCap);
+    {
+      uint32_t m = cmask;
+      uint32_t o = cbase + coff;
+      while (m) {
+        const uint32_t k = (uint32_t)(__ffs(m) - 1);
+        m &= m - 1u;
+        if (o < (uint32_t)kCandCap) cand[o] = ((uint64_t)__float_as_uint(Lt[k]) << 32) | (sc.lo + t * kResK + k);
+        ++o;
+      }
+    }
+    for (uint32_t i = t; i < kBins; i += kThreads) hl[i] = 0.f;
+    // the exact summands exp(v - m1), into this thread's LDS row
+#pragma unroll
+    for (int q = 0; q < (int)kResK / 4; ++q) {
+      const float e0 = expf_glibc_nonpos(__fsub_rn(x[4 * q], m1));
+      const float e1 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 1], m1));
+      const float e2 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 2], m1));
+      const float e3 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 3], m1));
+      *reinterpret_cast<float4*>(Lt + 4 * q) = make_float4(e0, e1, e2, e3);
+    }
+#ifdef LUMEN_RES_STOP
+    if (LUMEN_RES_STOP == 2) {
+      if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+      return;
+    }
+#endif
+    const uint32_t bsh = res_bin_shift(tau ? expf_glibc_nonpos(__fsub_rn(tv, m1)) : 0.f);
+    __syncthreads();  // the histogram is cleared
+    {
+      uint32_t m = cmask;
+      uint32_t o = cbase + coff;
+      while (m) {
+        const uint32_t k = (uint32_t)(__ffs(m) - 1);
+        m &= m - 1u;
+        const float ek = Lt[k];
+        if (o < (uint32_t)kCandCap) cande[o] = __float_as_uint(ek);
+        ++o;
+        atomicAdd(&hl[res_bin(ek, bsh)], ek);
+      }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < kBins; i += kThreads) hg[i] = hl[i];
+    const uint32_t nthr = (sc.hi - sc.lo + kResK - 1u) / kResK;
+    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, sl), s);
+    if (t == 0) {
+      ws.part_nrec[sl] = rc.ok ? rc.items : 0xffffffffu;
+      ws.part_nraw[sl] = rc.raws;
+    }
+  }
+  LUMEN_TICK("r_phaseB", b);
+  if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) return;
+  LUMEN_TICK("r_finisher", b);
+  RES_STOP(3);
+
+  // ---- finisher ----
+  // per-slice record sizes (one slice per lane of wave 0)
+  uint32_t* ib = s.H0;       // [G + 1] first item of each slice
+  uint32_t* rb = s.H0 + 32;  // [G + 1] first raw slot
+  if (t < 64u) {
+    const bool in = lane < G;
+    const uint32_t ni = in ? ws.part_nrec[lane] : 0u;
+    const uint32_t nr = in ? ws.part_nraw[lane] : 0u;
+    const bool failed = __ballot(in && ni == 0xffffffffu) != 0ull;
+    const uint32_t ei = wave_scan_incl(failed ? 0u : ni, 0u, op_add_u32);
+    const uint32_t er = wave_scan_incl(nr, 0u, op_add_u32);
+    const uint32_t pi = wave_shr1(ei, 0u), pr = wave_shr1(er, 0u);
+    if (lane <= G) {
+      ib[lane] = pi;
+      rb[lane] = pr;
+    }
+    if (lane == 0) s.misc_u[3] = failed ? 1u : 0u;
+  }
+  __syncthreads();
+  const uint32_t nit = ib[G], nrw = rb[G];
+  const uint32_t rawbase = 4u * nit;  // LDS word offset of the raws (s.Bk)
+  bad = bad || s.misc_u[3] != 0u || rawbase + kResK * nrw > 2u * (uint32_t)kCap ||
+        __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+  if (bad) {
+    row_single(a, b, s);
+    return;
+  }
+  // Gather, every load issued before any store (one round trip): the
+  // records (items, then raws) into s.Bk, the summed mass histogram into
+  // s.H, the candidates (logit bits << 32) | id into list A.
+  constexpr uint32_t kPer = (uint32_t)kCandCap / (uint32_t)kThreads;
+  {
+    uint32_t* words = reinterpret_cast<uint32_t*>(s.Bk);
+    const uint32_t nw = rawbase + kResK * nrw;
+    auto src_of = [&](uint32_t f) -> const uint32_t* {
+      uint32_t i = 0;
+      if (f < rawbase) {
+        const uint32_t it = f >> 2;
+        while (i + 1u < G && ib[i + 1] <= it) ++i;
+        return res_rec(a, b, i) + 4u * (it - ib[i]) + (f & 3u);
+      }
+      const uint32_t r = (f - rawbase) / kResK;
+      while (i + 1u < G && rb[i + 1] <= r) ++i;
+      return res_rec(a, b, i) + kResRawOff + kResK * (r - rb[i]) + (f - rawbase) % kResK;
+    };
+    constexpr int kWq = 4;
+    uint32_t wv[kWq];
+#pragma unroll
+    for (int q = 0; q < kWq; ++q) {
+      const uint32_t f = t + (uint32_t)q * kThreads;
+      wv[q] = f < nw ? *src_of(f) : 0u;
+    }
+    uint64_t cv[kPer];
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q) {
+      const uint32_t f = t + (uint32_t)q * kThreads;
+      cv[q] = f < ncand ? cand[f] : 0ull;
+    }
+    float hs = 0.f;
+    if (t < kBins) {
+      const float* hp = a.hist + (uint64_t)b * kMaxSlices * kMassBins + t;
+      float hv[kMaxSlices];
+#pragma unroll
+      for (uint32_t i = 0; i < (uint32_t)kMaxSlices; ++i) hv[i] = i < G ? hp[(uint64_t)i * kMassBins] : 0.f;
+#pragma unroll
+      for (uint32_t i = 0; i < (uint32_t)kMaxSlices; ++i) hs += hv[i];
+    }
+    for (uint32_t f0 = kWq * kThreads; f0 < nw; f0 += kWq * kThreads) {  // long records (rare)
+      uint32_t xv[kWq];
+#pragma unroll
+      for (int q = 0; q < kWq; ++q) {
+        const uint32_t f = f0 + t + (uint32_t)q * kThreads;
+        xv[q] = f < nw ? *src_of(f) : 0u;
+      }
+#pragma unroll
+      for (int q = 0; q < kWq; ++q) {
+        const uint32_t f = f0 + t + (uint32_t)q * kThreads;
+        if (f < nw) words[f] = xv[q];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kWq; ++q) {
+      const uint32_t f = t + (uint32_t)q * kThreads;
+      if (f < nw) words[f] = wv[q];
+    }
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q) {
+      const uint32_t f = t + (uint32_t)q * kThreads;
+      if (f < ncand) s.A[f] = cv[q];
+    }
+    if (t < kBins) reinterpret_cast<float*>(s.H)[t] = hs;
+    __syncthreads();
+  }
+  LUMEN_TICK("r_gathered", b);
+  RES_STOP(4);
+  // exact S1: the records in row order from 0, on wave 0; 64 items at a
+  // time sit in the lanes' registers, the walk reads them with readlane
+  if (t < 64u) {
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
+    const uint4* items = reinterpret_cast<const uint4*>(words);
+    const float* raws = reinterpret_cast<const float*>(words + rawbase);
+    uint32_t cb = 0u;  // bits of the exact running sum
+    uint32_t good = 1;
+    for (uint32_t k0 = 0; k0 < nit && good; k0 += 64u) {
+      const uint32_t k = k0 + lane;
+      uint4 it = make_uint4(0u, 0u, 0u, kNoRaw);
+      uint32_t roff = kNoRaw;
+      if (k < nit) {
+        it = items[k];
+        if (it.w != kNoRaw) {
+          uint32_t i = 0;
+          while (i + 1u < G && ib[i + 1] <= k) ++i;
+          roff = kResK * (rb[i] + it.w);
+        }
+      }
+      const uint32_t cnt = min(64u, nit - k0);
+      for (uint32_t q = 0; q < cnt; ++q) {
+        const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
+        const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
+        const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
+        const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
+        const uint32_t inc = (cb & 1u) ? a1 : a0;
+        if ((cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u) {
+          cb += inc;
+        } else if (ro != kNoRaw) {
+          const float4* r4 = reinterpret_cast<const float4*>(raws + ro);
+          float4 f[kResK / 4];
+#pragma unroll
+          for (int m = 0; m < (int)kResK / 4; ++m) f[m] = r4[m];
+          float c = __uint_as_float(cb);
+#pragma unroll
+          for (int m = 0; m < (int)kResK / 4; ++m) {
+            c = __fadd_rn(c, f[m].x);
+            c = __fadd_rn(c, f[m].y);
+            c = __fadd_rn(c, f[m].z);
+            c = __fadd_rn(c, f[m].w);
+          }
+          cb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(c));
+        } else {
+          good = 0;
+          break;
+        }
+      }
+    }
+    if (lane == 0) {
+      s.red_f[0] = __uint_as_float(cb);
+      s.misc_u[3] = good;
+    }
+  }
+  __syncthreads();
+  const float S1 = s.red_f[0];
+  const bool walked = s.misc_u[3] != 0u;
+  __syncthreads();
+  LUMEN_TICK("r_S1", b);
+  RES_STOP(5);
+  if (!walked) {
+    row_single(a, b, s);
+    return;
+  }
+  // Window: the lowest mass bin (from the top) whose running mass reaches
+  // top_p * S1 with a margin, plus one spare bin, bounds the window from
+  // below at p_lo. Every logit >= tv is a candidate, so every token with
+  // p > p(tv) is one: p_lo stays above p(tv).
+  const float e_tv = tau ? expf_glibc_nonpos(__fsub_rn(tv, m1)) : 0.f;
+  const uint32_t bsh = res_bin_shift(e_tv);
+  if (t < 64u) {
+    const float* hm = reinterpret_cast<const float*>(s.H);
+    const float target = fminf(__fmul_rn(__fmul_rn(P.top_p, S1), 1.004f), S1);
+    float run = 0.f;
+    uint32_t hit = kBins;
+    for (uint32_t base = 0; base < kBins && hit == kBins; base += 64u) {
+      const float m = wave_scan_incl(hm[base + t], 0.f, [](float l, float r) { return l + r; });
+      const unsigned long long hmsk = __ballot(run + m >= target);
+      if (hmsk) hit = base + (uint32_t)(__ffsll((long long)hmsk) - 1);
+      run += wave_read(m, 63);
+    }
+    if (t == 0) s.misc_u[2] = hit;
+  }
+  __syncthreads();
+  float p_lo;
+  {
+    const uint32_t hit = s.misc_u[2];
+    const float e_edge = hit + 1u < kBins ? res_bin_lo(hit + 1u, bsh) : 0.f;
+    p_lo = __fdiv_rn(fmaxf(e_edge, e_tv), S1);
+    if (tau) {
+      const float p_tv = __fdiv_rn(e_tv, S1);
+      if (!(p_lo > p_tv)) p_lo = __uint_as_float(__float_as_uint(p_tv) + 1u);
+    }
+  }
+  // the window's sort keys (~p << 32) | f in list B (f, the candidate's
+  // position, orders like its id); candidates 8t .. 8t+7 per thread
+  // (contiguous, so one block scan keeps index order)
+  uint32_t wmask = 0;
+  float pj[kPer];
+  {
+    const uint32_t* cande = reinterpret_cast<const uint32_t*>(cand + kCandCap);
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q) {
+      const uint32_t f = kPer * t + (uint32_t)q;
+      pj[q] = f < ncand ? __uint_as_float(cande[f]) : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q) {
+      pj[q] = __fdiv_rn(pj[q], S1);
+      wmask |= (pj[q] > 0.f && pj[q] >= p_lo ? 1u : 0u) << q;
+    }
+  }
+  uint32_t nw;
+  uint32_t wo = block_excl_scan_u32((uint32_t)__popc(wmask), s, &nw);
+  if (nw <= kResWindowCap) {
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q)
+      if ((wmask >> q) & 1u) s.Bk[wo++] = ((uint64_t)(~__float_as_uint(pj[q])) << 32) | (kPer * t + (uint32_t)q);
+  }
+  __syncthreads();
+  LUMEN_TICK("r_window", b);
+  RES_STOP(6);
+  if (nw > kResWindowCap || nw == 0u) {
+    row_single(a, b, s);
+    return;
+  }
+  {
+    const uint32_t khi = ~__float_as_uint(__fdiv_rn(1.0f, S1)), klo = ~__float_as_uint(p_lo);
+    const uint64_t hint = ((uint64_t)(khi ^ klo) << 32) | span_mask(kCandCap);
+    sort_u64_asc(s.Bk, nw, s.Bk + kResWindowCap, s, hint);
+  }
+  LUMEN_TICK("r_sorted", b);
+  RES_STOP(7);
+  const EcssResult wk = list_ecss_block(
+      nw, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe, P.top_p, 0.f, s);
+  LUMEN_TICK("r_crossing", b);
+  RES_STOP(8);
+  if (!wk.found) {
+    row_single(a, b, s);
+    return;
+  }
+  // the nucleus: the sorted window's first wk.pos + 1 entries, marked in a
+  // bitmap by candidate position, then compacted in index order into list A
+  // as (idx << 32) | key
+  uint32_t* kbits = s.H;  // [kCandCap / 32]
+  for (uint32_t i = t; i < (uint32_t)kCandCap / 32u; i += kThreads) kbits[i] = 0u;
+  __syncthreads();
+  for (uint32_t j = t; j <= (uint32_t)wk.pos; j += kThreads) {
+    const uint32_t f = (uint32_t)s.Bk[j];
+    atomicOr(&kbits[f >> 5], 1u << (f & 31u));
+  }
+  __syncthreads();
+  uint32_t nk;
+  {
+    const uint32_t kmask = (kbits[t >> 2] >> (8u * (t & 3u))) & 0xffu;  // candidates 8t .. 8t+7
+    uint64_t cv[kPer];
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q) cv[q] = (kmask >> q) & 1u ? s.A[kPer * t + (uint32_t)q] : 0ull;
+    uint32_t ko = block_excl_scan_u32((uint32_t)__popc(kmask), s, &nk);
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q)
+      if ((kmask >> q) & 1u)
+        s.A[ko++] = ((uint64_t)(uint32_t)cv[q] << 32) | tkey(__uint_as_float((uint32_t)(cv[q] >> 32)));
+    __syncthreads();
+  }
+  RowTrace tr;
+  init_trace(tr, V);
+  tr.path = 4u | 2u;
+  tr.passes = 1;
+  tr.windows = 1;
+  tr.topp_sum = S1;
+  tr.topp_kept = (uint32_t)wk.pos + 1u;
+  tr.topp_cum = wk.c;
+  tr.pad[0] = nit | (nrw << 16);
+  tr.pad[1] = ncand | (nw << 16);
+  LUMEN_TICK("r_kept", b);
+  RES_STOP(9);
+  // the nucleus holds the row maximum m1 (the largest p)
+  const uint32_t tok = final_on_list(a, P, nk, rdraw, s, tr, m1);
+  LUMEN_TICK("r_final", b);
+  write_result(a, b, tok, tr);
+}
+
+}  // namespace lumen

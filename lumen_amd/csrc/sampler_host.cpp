@@ -36,11 +36,14 @@ namespace {
 // dispatch in lumen_sample_rows).
 enum RowPath { kPathGreedy, kPathTopK, kPathTopP, kPathSingle };
 constexpr uint32_t kWgThreads = 1024;  // lumen_sample_rows workgroup size
+constexpr uint32_t kResSlice = 32u * kWgThreads;  // logits per register-resident slice
 
 RowPath row_path(const RowParams& r, uint32_t V, uint32_t G) {
   if (r.flags & lumen::kGreedy) return kPathGreedy;
   if ((r.flags & lumen::kTopK) && r.top_k <= 2048u) return kPathTopK;
   const uint32_t per = G ? ((V + G - 1u) / G + 15u) & ~15u : V;
+  // register-resident top-p slices (any penalties, min-p, temperature)
+  if ((r.flags & lumen::kTopP) && !(r.flags & lumen::kTopK) && per <= kResSlice) return kPathTopP;
   if ((r.flags & lumen::kTopP) && !(r.flags & (lumen::kTopK | lumen::kPen)) &&
       per <= 32u * kWgThreads * (uint32_t)lumen::kChainMaxQ)
     return kPathTopP;
@@ -61,9 +64,6 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
   const uint32_t kX = 8;
   const uint32_t bin_cap = cap / kX;
   std::vector<uint32_t> G(B, 1), w(B, 0);
-  const uint32_t gmin_topp =
-      (V + 32u * kWgThreads * (uint32_t)lumen::kChainMaxQ - 1u) /
-      (32u * kWgThreads * (uint32_t)lumen::kChainMaxQ);
   // slice weights of the greedy, top-k and top-p paths; LUMEN_SAMPLER_WEIGHTS=g,k,p
   // overrides them (a tuning aid)
   struct Weights {
@@ -93,7 +93,7 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
     if (!w[b]) continue;
     uint64_t g = wsum ? ((uint64_t)spare * w[b] + wsum / 2) / wsum : 1;
     G[b] = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(g, lumen::kMaxSlices));
-    if (row_path(rows[b], V, G[b]) == kPathTopP && G[b] < gmin_topp) G[b] = 1;
+    if (row_path(rows[b], V, G[b]) == kPathSingle) G[b] = 1;
   }
   // every row at g_uniform: the kernel's arithmetic mapping places the same
   // grid without a map (one dependent load less per workgroup)
@@ -115,7 +115,6 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
     uint32_t free_slots = bin_cap > bins[best].size() ? bin_cap - (uint32_t)bins[best].size() : 0;
     uint32_t g = std::min(G[b], std::max<uint32_t>(free_slots, 1u));
     if (g > 1 && row_path(rows[b], V, g) == kPathSingle) g = 1;
-    if (g > 1 && row_path(rows[b], V, g) == kPathTopP && g < gmin_topp) g = 1;
     for (uint32_t sl = 0; sl < g; ++sl) bins[best].push_back((b << 10) | (g << 5) | sl);
   }
   size_t depth = 0;
@@ -147,7 +146,7 @@ struct lumen_sampler {
   DevBuf stage;
   DevBuf pen_scratch;
   DevBuf ws;    // [B] RowWs, zeroed at allocation, self-resetting afterwards
-  DevBuf cand;  // [B][kCandCap] candidate buffers
+  DevBuf cand;  // [B][kCandStride] candidate buffers
   DevBuf est;   // [B][kRowRecs][kRecWords] run records of the split top-p path
   DevBuf hist;  // [B][kMaxSlices][kMassBins] candidate mass histograms
   DevBuf guard;  // [B][kGuardWords] anti-restate candidates when the caller passes none
@@ -781,7 +780,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       // zero once at allocation; afterwards each launch leaves it zeroed
       if (hipMemset(s->ws.p, 0, s->ws.cap) != hipSuccess) return fail(LUMEN_ERR_HIP, "workspace init");
     }
-    int rc = ensure_dev(s->cand, sizeof(uint64_t) * lumen::kCandCap * B);
+    int rc = ensure_dev(s->cand, sizeof(uint64_t) * lumen::kCandStride * B);
     if (rc != LUMEN_OK) return rc;
     rc = ensure_dev(s->est, sizeof(uint32_t) * lumen::kRecWords * lumen::kRowRecs * B);
     if (rc != LUMEN_OK) return rc;

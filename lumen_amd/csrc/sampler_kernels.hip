@@ -256,6 +256,28 @@ __device__ __forceinline__ float block_rmax(float v, Smem& s) {
   return r;
 }
 
+// block_rmax together with a NaN flag (one barrier pair).
+__device__ __forceinline__ float block_rmax_nan(float v, bool nan, Smem& s, bool* any_nan) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_reduce(v, kNegInf, rmax);
+  const bool wn = __ballot(nan) != 0ull;
+  if (lane == 0) {
+    s.red_f[w] = v;
+    s.red_b[w] = wn ? 1u : 0u;
+  }
+  __syncthreads();
+  float r = kNegInf;
+  uint32_t n = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    r = rmax(r, s.red_f[i]);
+    n |= s.red_b[i];
+  }
+  __syncthreads();
+  *any_nan = n != 0u;
+  return r;
+}
+
 __device__ __forceinline__ uint32_t block_incl_scan_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   v = wave_scan_incl(v, 0u, op_add_u32);
@@ -733,6 +755,40 @@ __device__ __forceinline__ EcssResult list_ecss(uint32_t n, X&& xf, int mode, fl
   }
 }
 
+// The same on the whole workgroup, 4096 elements at a time (thread t holds
+// elements 4t .. 4t+3 of a chunk), with the estimate-guided chunk method of
+// ecss.h: each chunk starts from the exact running sum, so its drift bound
+// is rigorous, and one segmented scan plus a short walk over the few
+// threads near a binade edge replaces a wave scan per edge.
+template <class X>
+__device__ __forceinline__ EcssResult list_ecss_block(uint32_t n, X&& xf, int mode, float theta,
+                                                      float c0, Smem& s) {
+  constexpr int M = 4;
+  float c = c0;
+  for (uint32_t base = 0; base < n; base += (uint32_t)kThreads * M) {
+    float x[M];
+#pragma unroll
+    for (int q = 0; q < M; ++q) {
+      const uint32_t j = base + threadIdx.x * M + (uint32_t)q;
+      x[q] = j < n ? xf(j) : 0.f;
+    }
+    EcssResult e = ecss_chunk4(c, x, mode, theta,
+                               (int)min((uint32_t)kThreads, (n - base + (uint32_t)M - 1u) / (uint32_t)M),
+                               s.ecss, s.est);
+    if (e.found) {
+      e.pos += (int)base;
+      return e;
+    }
+    c = e.c;
+  }
+  EcssResult e;
+  e.c = c;
+  e.found = 0;
+  e.pos = -1;
+  e.before = 0.f;
+  return e;
+}
+
 // Walk over V tokens that all carry the same probability u (the uniform
 // branch of softmax, sampling.rs:211-214 and :224-227).
 __device__ __forceinline__ EcssResult const_ecss(uint32_t V, float u, int mode, float theta, Smem& s) {
@@ -920,15 +976,24 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
   // the summands, then the probabilities, computed by the whole workgroup
   // into LDS (list B is free here); the exact sums read them back
   float* xs = reinterpret_cast<float*>(s.Bk);
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[pad16(j)] = expf_glibc(__fsub_rn(wv(j), m3));
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = expf_glibc(__fsub_rn(wv(j), m3));
   __syncthreads();
-  EcssResult S = list_ecss(n, [&](uint32_t j) { return xs[pad16(j)]; }, kEcssSum, 0.f, 0.f, s);
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 20) return 0;
+#endif
+  EcssResult S = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssSum, 0.f, 0.f, s);
   const float S3 = S.c;
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[pad16(j)] = __fdiv_rn(xs[pad16(j)], S3);
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 21) return 0;
+#endif
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
   __syncthreads();
   LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", 0);
   tr.final_sum = S3;
-  EcssResult e = list_ecss(n, [&](uint32_t j) { return xs[pad16(j)]; }, kEcssFindGt, r, 0.f, s);
+  EcssResult e = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
+#ifdef LUMEN_RES_STOP
+  if (LUMEN_RES_STOP == 22) return 0;
+#endif
   LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", 0);
   LUMEN_TICK("fin_walk", 0);
   tr.cdf_before = e.found ? e.before : e.c;
@@ -947,194 +1012,266 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
 // general path (uniform branches, NaN, or a non-finite temperature product).
 constexpr uint32_t kWaveList = 256;
 
-// The reference's own sequential f32 loop over xs[0..n) (LDS), run by every
-// lane of the wave on broadcast reads, 16 loads ahead of the dependent adds.
-// For short lists this is cheaper than the parity-map method, whose cost
-// grows with the number of binades the sum crosses.
+// The reference's own sequential f32 loop over xs[0..n) (LDS, 16-byte
+// aligned, zero from n up to the next multiple of 32), run by every lane of
+// the wave on broadcast reads. The running sum never decreases, so a search
+// first adds whole blocks of 32 (the next block's loads in flight meanwhile)
+// and stops at the first block whose end meets the condition, then repeats
+// that block one element at a time. For short lists this is cheaper than
+// the parity-map method, whose cost grows with the binades the sum crosses.
 __device__ __forceinline__ EcssResult seq_ecss(const float* xs, uint32_t n, int mode, float theta) {
-  float c = 0.f, prev = 0.f;
-  int pos = -1;
-  for (uint32_t j0 = 0; j0 < n && pos < 0; j0 += 16u) {
-    float xv[16];
+  const float4* x4 = reinterpret_cast<const float4*>(xs);
+  const uint32_t nb = (n + 31u) >> 5;
+  float c = 0.f;
+  uint32_t hit = nb;
+  for (uint32_t bk = 0; bk < nb; ++bk) {
+    float4 cur[8];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) xv[q] = (j0 + (uint32_t)q < n) ? xs[j0 + q] : 0.f;
+    for (int m = 0; m < 8; ++m) cur[m] = x4[8u * bk + (uint32_t)m];
+    float y = c;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      if (pos < 0) {
-        const float y = __fadd_rn(c, xv[q]);
-        if (mode != kEcssSum && j0 + (uint32_t)q < n && ecss_cond(mode, y, theta)) {
-          pos = (int)(j0 + (uint32_t)q);
-          prev = c;
-        }
-        c = y;
-      }
+    for (int m = 0; m < 8; ++m) {
+      y = __fadd_rn(y, cur[m].x);
+      y = __fadd_rn(y, cur[m].y);
+      y = __fadd_rn(y, cur[m].z);
+      y = __fadd_rn(y, cur[m].w);
     }
+    if (mode != kEcssSum && ecss_cond(mode, y, theta)) {
+      hit = bk;
+      break;
+    }
+    c = y;
   }
   EcssResult r;
   r.c = c;
-  r.before = prev;
-  r.found = pos >= 0 ? 1 : 0;
-  r.pos = pos;
+  r.found = 0;
+  r.pos = -1;
+  r.before = 0.f;
+  if (hit == nb) return r;
+  // the hit block again: lane q keeps the sum before and after element q
+  const uint32_t lane = threadIdx.x & 63u;
+  float4 hb[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) hb[m] = x4[8u * hit + (uint32_t)m];
+  float y = c, mine = 0.f, pre = 0.f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float xq[4] = {hb[m].x, hb[m].y, hb[m].z, hb[m].w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float y1 = __fadd_rn(y, xq[u]);
+      pre = lane == (uint32_t)(4 * m + u) ? y : pre;
+      mine = lane == (uint32_t)(4 * m + u) ? y1 : mine;
+      y = y1;
+    }
+  }
+  const unsigned long long hm = __ballot(lane < 32u && ecss_cond(mode, mine, theta));
+  const int q = __ffsll((long long)hm) - 1;  // the block end met the condition: q >= 0
+  r.c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), q));
+  r.before = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pre), q));
+  r.found = 1;
+  r.pos = (int)(32u * hit) + q;
   return r;
 }
 
+#ifdef LUMEN_WSP_STOP
+__device__ int g_wsp_stop;
+#define WSP_STOP(k)                    \
+  do {                                 \
+    if (g_wsp_stop == (k)) return true; \
+  } while (0)
+#else
+#define WSP_STOP(k) do { } while (0)
+#endif
+
+// f32::max folded in index order (NaN excluded by the caller): between equal
+// values (+0 and -0) the later one wins, as in fold(-inf, f32::max).
+__device__ __forceinline__ float op_maxl(float l, float r) { return r >= l ? r : l; }
+
+// Maximum (f32::max in index order, NaN skipped) and NaN flag of one value
+// per thread over the first nw waves; every thread gets the result. Waves
+// at or past nw contribute nothing but must call it (two barriers).
+__device__ __forceinline__ float small_max(float v, bool valid, uint32_t nw, Smem& s, bool* any_nan) {
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  if (w < nw) {
+    const bool nn = valid && is_nan(v);
+    const float m = wave_reduce(nn || !valid ? kNegInf : v, kNegInf, op_maxl);
+    const bool wn = __ballot(nn) != 0ull;
+    if (lane == 0) {
+      s.red_f[w] = m;
+      s.red_b[w] = wn ? 1u : 0u;
+    }
+  }
+  __syncthreads();
+  float r = kNegInf;
+  uint32_t f = 0;
+  for (uint32_t i = 0; i < nw; ++i) {
+    r = op_maxl(r, s.red_f[i]);
+    f |= s.red_b[i];
+  }
+  __syncthreads();
+  *any_nan = f != 0u;
+  return r;
+}
+
+// Everything after top-k for a list of at most kWaveList entries (s.A,
+// (idx << 32) | key, ascending idx) whose maximum is finite and that holds
+// no NaN: thread j < n holds entry j (only the first nw = ceil(n / 64) waves
+// work, the others wait at the barriers); the four sequential sums run on
+// wave 0 (seq_ecss). Returns false (uniform), having written nothing and
+// left s.A as it was, when the list needs the general path (uniform
+// branches, NaN, or a non-finite temperature product).
 __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, const RowParams& P,
                                                 uint32_t n, bool topp_done, float r, Smem& s,
                                                 RowTrace& tr) {
-  const uint32_t t = threadIdx.x, V = a.vocab;
-  uint64_t* keys = s.Bk;          // [kWaveList] sort keys, then by rank
-  float* sp = reinterpret_cast<float*>(s.Bk + kWaveList);  // [kWaveList] p by rank
-  float* xs = sp + kWaveList;     // [kWaveList] summands in index order
-  if (t < 64u) do {
-    const uint32_t lane = t;
-    uint32_t idx[4];
-    float v[4];
-    bool val[4];
-    float m = kNegInf;
-    bool nan = false;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t j = 4u * lane + (uint32_t)q;
-      val[q] = j < n;
-      const uint64_t e = val[q] ? s.A[j] : 0ull;
-      idx[q] = (uint32_t)(e >> 32);
-      v[q] = val[q] ? key2f((uint32_t)e) : kNegInf;
-      nan |= val[q] && is_nan(v[q]);
-      m = rmax(m, v[q]);
+  const uint32_t t = threadIdx.x, V = a.vocab, lane = t & 63u, w = t >> 6;
+  const uint32_t nw = (n + 63u) >> 6;
+  const bool wact = w < nw;
+  float* xs = reinterpret_cast<float*>(s.Bk);  // [kWaveList] summands in index order
+  float* sp = xs + kWaveList;                   // [kWaveList] p by rank
+  float* pv = sp + kWaveList;                   // [kWaveList] p by index
+  uint32_t* rank = reinterpret_cast<uint32_t*>(pv + kWaveList);  // [kWaveList]
+  float* res = reinterpret_cast<float*>(rank + kWaveList);       // [8] results of wave 0
+  const bool act = t < n;
+  float v = kNegInf;
+  if (wact) {
+    if (act) v = key2f((uint32_t)s.A[t]);
+    // seq_ecss reads whole blocks of 32: zeros past the list
+    if (t >= n && t < ((n + 31u) & ~31u)) {
+      xs[t] = 0.f;
+      sp[t] = 0.f;
     }
-    m = wave_reduce(m, kNegInf, rmax);
-    nan = __ballot(nan) != 0ull;
-    bool ok = is_finite(m) && !nan;
-    bool kept[4] = {val[0], val[1], val[2], val[3]};
-    float tp_sum = 0.f, tp_cum = 0.f;
-    uint32_t tp_kept = 0;
-    const bool do_topp = ok && (P.flags & kTopP) && !topp_done;
-    if (do_topp) {
-      // top-p on the list (sampling.rs:942-967): softmax at T = 1 in index
-      // order, then the cumulative sum in (p desc, idx asc) order
-      float ex[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        ex[q] = val[q] ? expf_glibc(__fsub_rn(v[q], m)) : 0.f;
-        if (val[q]) xs[4u * lane + (uint32_t)q] = ex[q];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const float S1 = seq_ecss(xs, n, kEcssSum, 0.f).c;
-      uint64_t key[4];
-      float p[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        p[q] = val[q] ? __fdiv_rn(ex[q], S1) : 0.f;
-        key[q] = val[q] ? (((uint64_t)(~__float_as_uint(p[q])) << 32) | idx[q]) : ~0ull;
-        if (val[q]) keys[4u * lane + (uint32_t)q] = key[q];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // keys past n read as all-ones (never below a live key)
-      for (uint32_t j = n + lane; j < ((n + 15u) & ~15u); j += 64u) keys[j] = ~0ull;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      uint32_t rk[4] = {0u, 0u, 0u, 0u};
-      for (uint32_t i0 = 0; i0 < n; i0 += 16u) {
-        uint64_t kb[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) kb[u] = keys[i0 + (uint32_t)u];
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) rk[q] += kb[u] < key[q] ? 1u : 0u;
-      }
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (val[q]) sp[rk[q]] = p[q];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const EcssResult w = seq_ecss(sp, n, kEcssFindGe, P.top_p);
-      tp_sum = S1;
-      tp_cum = w.c;
-      tp_kept = w.found ? (uint32_t)w.pos + 1u : V;
-      if (w.found) {
-        // the entry at sorted position w.pos: the one whose rank equals it
-        uint64_t kst = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) kst = (val[q] && rk[q] == (uint32_t)w.pos) ? key[q] : kst;
-        kst = wave_reduce(kst, (uint64_t)0, op_max_u64);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) kept[q] = val[q] && key[q] <= kst;
-      }
+    rank[t] = 0u;
+  }
+  bool nan;
+  const float m = small_max(v, act, nw, s, &nan);
+  if (!is_finite(m) || nan) return false;
+  WSP_STOP(1);
+  bool kept = act;
+  float tp_sum = 0.f, tp_cum = 0.f;
+  uint32_t tp_kept = 0;
+  const bool do_topp = (P.flags & kTopP) && !topp_done;
+  if (do_topp) {
+    // top-p on the list (sampling.rs:942-967): softmax at T = 1 in index
+    // order, then the cumulative sum in (p desc, idx asc) order
+    float ex = 0.f;
+    if (wact) {
+      ex = act ? expf_glibc(__fsub_rn(v, m)) : 0.f;
+      if (act) xs[t] = ex;
     }
-    // min-p (sampling.rs:976-994): the bound comes from the surviving
-    // maximum, which top-p always keeps (it has the largest p)
-    if (ok && (P.flags & kMinP)) {
-      const float bound = __fadd_rn(m, P.log_min_p);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) kept[q] = kept[q] && !(v[q] < bound);
+    __syncthreads();
+    if (t < 64u) {
+      const float S1w = seq_ecss(xs, n, kEcssSum, 0.f).c;
+      if (lane == 0) res[0] = S1w;
     }
-    // temperature, softmax, inverse-CDF draw (sampling.rs:516-526, 1003-1014)
-    float wv[4];
-    float m3 = kNegInf;
-    bool nan3 = false;
+    __syncthreads();
+    const float S1 = res[0];
+    const float p = act ? __fdiv_rn(ex, S1) : 0.f;
+    if (act) pv[t] = p;
+    if (wact && t >= n) pv[t] = 0.f;
+    __syncthreads();
+    WSP_STOP(2);
+    // rank of entry j in (p desc, idx asc) order: keys (~p << 32) | j (the
+    // list is in idx order), four threads per entry, each over a quarter
+    // of the list, 16 keys at a time
+    {
+      const uint32_t j = t & (kWaveList - 1u), g = t / kWaveList;
+      const uint32_t i0 = g * (kWaveList / 4u), i1 = min(n, i0 + kWaveList / 4u);
+      if (j < ((n + 63u) & ~63u) && i0 < i1) {
+        const uint64_t kj = ((uint64_t)(~__float_as_uint(j < n ? pv[j] : 0.f)) << 32) | j;
+        uint32_t c = 0;
+        for (uint32_t ib = i0; ib < i1; ib += 16u) {
+          const float4* p4 = reinterpret_cast<const float4*>(pv + ib);
+          float4 q[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      wv[q] = kept[q] ? __fmul_rn(v[q], P.inv_temp) : kNegInf;
-      nan3 |= kept[q] && is_nan(wv[q]);
-      m3 = rmax(m3, wv[q]);
-    }
-    m3 = wave_reduce(m3, kNegInf, rmax);
-    ok = ok && is_finite(m3) && __ballot(nan3) == 0ull;
-    if (ok) {
-      float e3[4];
+          for (int u = 0; u < 4; ++u) q[u] = p4[u];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        e3[q] = kept[q] ? expf_glibc(__fsub_rn(wv[q], m3)) : 0.f;
-        if (val[q]) xs[4u * lane + (uint32_t)q] = e3[q];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const float S3 = seq_ecss(xs, n, kEcssSum, 0.f).c;
-      __builtin_amdgcn_wave_barrier();
+          for (int u = 0; u < 4; ++u) {
+            const float qq[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (val[q]) xs[4u * lane + (uint32_t)q] = kept[q] ? __fdiv_rn(e3[q], S3) : 0.f;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const EcssResult e = seq_ecss(xs, n, kEcssFindGt, r);
-      uint32_t tok = V - 1u;
-      if (e.found) {
-        const int qq = e.pos & 3;
-        const uint32_t ix = qq == 0 ? idx[0] : qq == 1 ? idx[1] : qq == 2 ? idx[2] : idx[3];
-        tok = (uint32_t)__builtin_amdgcn_readlane((int)ix, e.pos >> 2);
-      }
-      if (lane == 0) {
-        tr.path |= 2u;
-        if (do_topp) {
-          tr.topp_sum = tp_sum;
-          tr.topp_kept = tp_kept;
-          tr.topp_cum = tp_cum;
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t i = ib + 4u * (uint32_t)u + (uint32_t)e;
+              const uint64_t ki = ((uint64_t)(~__float_as_uint(qq[e])) << 32) | (i < i1 ? i : 0xffffffffu);
+              c += ki < kj ? 1u : 0u;
+            }
+          }
         }
-        tr.final_max = m3;
-        tr.final_sum = S3;
-        tr.cdf_before = e.found ? e.before : e.c;
-        tr.cdf_at = e.c;
-        s.misc_u[0] = tok;
+        if (c && j < n) atomicAdd(&rank[j], c);
       }
     }
-    if (lane == 0) s.misc_u[1] = ok ? 1u : 0u;
-  } while (0);
+    __syncthreads();
+    const uint32_t rk = act ? rank[t] : 0u;
+    if (act) sp[rk] = p;
+    __syncthreads();
+    WSP_STOP(3);
+    if (t < 64u) {
+      const EcssResult wr = seq_ecss(sp, n, kEcssFindGe, P.top_p);
+      if (lane == 0) {
+        res[1] = wr.c;
+        reinterpret_cast<int*>(res)[2] = wr.found ? wr.pos : -1;
+      }
+    }
+    __syncthreads();
+    const int wpos = reinterpret_cast<const int*>(res)[2];
+    tp_sum = S1;
+    tp_cum = res[1];
+    tp_kept = wpos >= 0 ? (uint32_t)wpos + 1u : V;
+    if (wpos >= 0) kept = act && rk <= (uint32_t)wpos;
+    WSP_STOP(4);
+  }
+  // min-p (sampling.rs:976-994): the bound comes from the surviving
+  // maximum, which top-p always keeps (it has the largest p)
+  if (P.flags & kMinP) {
+    const float bound = __fadd_rn(m, P.log_min_p);
+    kept = kept && !(v < bound);
+  }
+  // temperature, softmax, inverse-CDF draw (sampling.rs:516-526, 1003-1014)
+  const float wv = kept ? __fmul_rn(v, P.inv_temp) : kNegInf;
+  bool nan3 = false;
+  // Without min-p the kept set holds the list maximum m (top-p keeps the
+  // largest p), and x -> x * inv_temp is monotone under rounding for
+  // inv_temp > 0, so its maximum is m * inv_temp; a non-finite product
+  // (inv_temp = inf) takes the general path below.
+  const float m3 = (P.flags & kMinP) ? small_max(wv, kept, nw, s, &nan3) : __fmul_rn(m, P.inv_temp);
+  if (!is_finite(m3) || nan3) return false;  // list and s.A untouched: the general path redoes it
+  WSP_STOP(5);
+  float e3 = 0.f;
+  if (wact) {
+    e3 = kept ? expf_glibc(__fsub_rn(wv, m3)) : 0.f;
+    if (act) xs[t] = e3;
+  }
   __syncthreads();
-  const bool handled = s.misc_u[1] != 0u;
-  const uint32_t tok = s.misc_u[0];
+  if (t < 64u) {
+    const float S3w = seq_ecss(xs, n, kEcssSum, 0.f).c;
+    if (lane == 0) res[3] = S3w;
+  }
   __syncthreads();
-  if (handled) write_result(a, b, tok, tr);
-  return handled;
+  const float S3 = res[3];
+  WSP_STOP(6);
+  if (act) xs[t] = kept ? __fdiv_rn(e3, S3) : 0.f;
+  __syncthreads();
+  if (t < 64u) {
+    const EcssResult ec = seq_ecss(xs, n, kEcssFindGt, r);
+    if (lane == 0) {
+      res[4] = ec.found ? ec.before : ec.c;
+      res[5] = ec.c;
+      reinterpret_cast<uint32_t*>(res)[6] = ec.found ? (uint32_t)(s.A[ec.pos] >> 32) : V - 1u;
+    }
+  }
+  __syncthreads();
+  WSP_STOP(7);
+  tr.path |= 2u;
+  if (do_topp) {
+    tr.topp_sum = tp_sum;
+    tr.topp_kept = tp_kept;
+    tr.topp_cum = tp_cum;
+  }
+  tr.final_max = m3;
+  tr.final_sum = S3;
+  tr.cdf_before = res[4];
+  tr.cdf_at = res[5];
+  write_result(a, b, reinterpret_cast<const uint32_t*>(res)[6], tr);
+  return true;
 }
 
 // Everything after top-k for a row whose survivors are in s.A as
@@ -2381,7 +2518,7 @@ __device__ __forceinline__ void slice_pen_out(const KernelArgs& a, int b, const 
   const RowParams P = (a).inline_rows ? (a).inline_params[b] : (a).params[b];         \
   const float rdraw = row_draw((a), (b));                                             \
   RowWs& ws = (a).ws[b];                                                              \
-  uint64_t* cand = (a).cand + (uint64_t)(b) * kCandCap;                               \
+  uint64_t* cand = (a).cand + (uint64_t)(b) * kCandStride;                            \
   const Row row = make_row((a), (b));                                                 \
   (void)rdraw;                                                                        \
   (void)cand
@@ -3369,6 +3506,12 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   small_path(a, b, P, nk, true, rdraw, s, tr, m1);
 }
 
+}  // namespace lumen
+
+#include "resident.h"
+
+namespace lumen {
+
 // Row and slice of this workgroup. With xcd_rows, blocks are dispatched to
 // the 8 XCDs round-robin: a row's slices stay on one XCD so its
 // coordination traffic stays in that XCD's L2.
@@ -3448,6 +3591,12 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
         greedy_split(a, (int)b, sl, G, s);
     } else if ((flags & kTopK) && top_k <= 2048u) {
       topk_split(a, (int)b, sl, G, s);
+    } else if ((flags & kTopP) && !(flags & kTopK) && per <= kResSlice && a.vocab >= 64u &&
+               make_row(a, (int)b).vec) {
+      if (a.dtype == 0)
+        topp_res<false>(a, (int)b, sl, G, s);
+      else
+        topp_res<true>(a, (int)b, sl, G, s);
     } else if ((flags & kTopP) && !(flags & (kTopK | kPen)) &&
                per <= 32u * kThreads * kChainMaxQ) {
       topp_split(a, (int)b, sl, G, s);
