@@ -199,6 +199,20 @@ void lumen_sampler_destroy(lumen_sampler *s);
  * (compute/mod.rs:424-438). */
 int lumen_sampler_sample_batch(lumen_sampler *s, const lumen_batch *batch, lumen_stream stream);
 
+/* The same as lumen_sampler_sample_batch, allocating nothing: no device or
+ * pinned memory is allocated, by the library or by a library it calls. No
+ * counterpart in the reference; it is for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. Its device buffers are carved from one 32 MiB array per GPU in
+ * the library itself, so a call takes at most 8 rows of at most 262144
+ * logits, no device history (hist_ring_dev), at most 65536 form-A penalty
+ * entries, and anti_restate rows need guard_out; anything beyond returns
+ * LUMEN_ERR_INVALID with lumen_sampler_last_error() naming the limit. Every
+ * call on a GPU shares that GPU's array (from every context and thread):
+ * calls that overlap on one GPU race, so serialize them (one stream). */
+int lumen_sampler_sample_batch_noalloc(lumen_sampler *s, const lumen_batch *batch,
+                                       lumen_stream stream);
+
 /* Synchronous convenience: same as above, then waits and copies the tokens
  * to host memory. Returns LUMEN_ERR_ROW if a row reported a failure.
  * Mirrors Sampler::sample / sample_token_with_state (sampling.rs:429-433,

@@ -28,6 +28,7 @@ EXPORTS = (
     "lumen_sampler_create",
     "lumen_sampler_destroy",
     "lumen_sampler_sample_batch",
+    "lumen_sampler_sample_batch_noalloc",
     "lumen_sampler_sample_batch_sync",
     "lumen_xorshift64_new",
     "lumen_xorshift64_next_u64",
@@ -134,6 +135,8 @@ def load():
     L.lumen_sampler_sample_batch.restype = ctypes.c_int
     L.lumen_sampler_sample_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(BatchC),
                                              ctypes.c_void_p]
+    L.lumen_sampler_sample_batch_noalloc.restype = ctypes.c_int
+    L.lumen_sampler_sample_batch_noalloc.argtypes = L.lumen_sampler_sample_batch.argtypes
     L.lumen_sampler_sample_batch_sync.restype = ctypes.c_int
     L.lumen_sampler_sample_batch_sync.argtypes = [ctypes.c_void_p, ctypes.POINTER(BatchC),
                                                   ctypes.POINTER(ctypes.c_uint32),

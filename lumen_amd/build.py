@@ -56,13 +56,20 @@ def build(verbose: bool = False) -> str:
     obj = os.path.join(LIB, "code_object.o")
     _run(["gcc", "-c", f'-DLUMEN_HSACO_PATH="{HSACO}"', "-o", obj,
           os.path.join(CSRC, "code_object.S")])
+    # the no-allocation entry point's device array lives in a HIP source of
+    # the host library (its own gfx950 device code, registered by HIP)
+    na_obj = os.path.join(LIB, "noalloc.o")
+    _run([hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-c",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-o", na_obj, os.path.join(CSRC, "noalloc.hip")])
     tmp_so = SO + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f"-I{ROOT}/include",
-          "-o", tmp_so, os.path.join(CSRC, "sampler_host.cpp"), obj,
+          "-o", tmp_so, os.path.join(CSRC, "sampler_host.cpp"), obj, na_obj,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
     os.replace(tmp_so, SO)
     os.remove(obj)
+    os.remove(na_obj)
     if verbose:
         print("built", SO)
     return SO

@@ -23,6 +23,7 @@
 
 #include "../../include/lumen_sampler.h"
 #include "kernel_abi.h"
+#include "noalloc.h"
 
 extern "C" const unsigned char lumen_gfx950_code_object[];
 extern "C" const unsigned char lumen_gfx950_code_object_end[];
@@ -140,6 +141,7 @@ struct lumen_sampler {
   hipModule_t module = nullptr;
   hipFunction_t fn = nullptr;
   hipFunction_t fn_hist = nullptr;  // lumen_hist_window
+  hipFunction_t fn_zero = nullptr;  // lumen_zero_tokens (no-allocation entry, empty vocabulary)
   // staging: one pinned host block and one device block, same layout
   void* pin = nullptr;
   size_t pin_cap = 0;
@@ -448,7 +450,8 @@ int lumen_sampler_create(lumen_sampler** out, int device) {
     return LUMEN_ERR_CODE_OBJECT;
   }
   if (hipModuleGetFunction(&s->fn, s->module, "lumen_sample_rows") != hipSuccess ||
-      hipModuleGetFunction(&s->fn_hist, s->module, "lumen_hist_window") != hipSuccess) {
+      hipModuleGetFunction(&s->fn_hist, s->module, "lumen_hist_window") != hipSuccess ||
+      hipModuleGetFunction(&s->fn_zero, s->module, "lumen_zero_tokens") != hipSuccess) {
     (void)hipGetLastError();
     (void)hipModuleUnload(s->module);
     delete s;
@@ -462,6 +465,16 @@ int lumen_sampler_create(lumen_sampler** out, int device) {
     if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, s->fn, 1024, 0) != hipSuccess)
       per_cu = 0;
     s->max_resident = per_cu * s->cu_count;
+  }
+  {
+    // the no-allocation entry point's scratch array on this device
+    void* na = nullptr;
+    if (lumen::noalloc_scratch(&na) != hipSuccess) {
+      (void)hipGetLastError();
+      (void)hipModuleUnload(s->module);
+      delete s;
+      return LUMEN_ERR_HIP;
+    }
   }
   if (hipEventCreateWithFlags(&s->staged, hipEventDisableTiming) != hipSuccess) {
     (void)hipModuleUnload(s->module);
@@ -493,18 +506,40 @@ void lumen_sampler_destroy(lumen_sampler* s) {
 
 namespace {
 int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, uint32_t* tok_map,
-                 uint32_t* done_map, uint32_t* guard_map, bool sync);
+                 uint32_t* done_map, uint32_t* guard_map, bool sync, bool noalloc = false);
 }  // namespace
 
 int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream) {
   return launch_batch(s, bt, stream, nullptr, nullptr, nullptr, false);
 }
 
+int lumen_sampler_sample_batch_noalloc(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream) {
+  return launch_batch(s, bt, stream, nullptr, nullptr, nullptr, false, true);
+}
+
 namespace {
+// Device buffers of the no-allocation entry point, carved in order from the
+// scratch array (256-byte aligned pieces).
+struct Arena {
+  char* base = nullptr;
+  size_t used = 0;
+  void* take(size_t bytes) {
+    const size_t at = (used + 255) & ~size_t(255);
+    if (at + bytes > lumen::kNoAllocBytes) return nullptr;
+    used = at + bytes;
+    return base + at;
+  }
+};
+
 int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, uint32_t* tok_map,
-                 uint32_t* done_map, uint32_t* guard_map, bool sync) {
+                 uint32_t* done_map, uint32_t* guard_map, bool sync, bool noalloc) {
   if (!s || !bt) return fail(LUMEN_ERR_INVALID, "null context or batch");
   const uint32_t B = bt->batch, V = bt->vocab;
+  if (noalloc) {
+    if (B > lumen::kNoAllocMaxRows) return fail(LUMEN_ERR_INVALID, "noalloc: batch must be at most 8 rows");
+    if (V > lumen::kNoAllocMaxVocab) return fail(LUMEN_ERR_INVALID, "noalloc: vocab must be at most 262144");
+    if (bt->hist_ring_dev) return fail(LUMEN_ERR_INVALID, "noalloc: hist_ring_dev is not supported");
+  }
   if (B == 0) return LUMEN_OK;
   if (!bt->params || !bt->tokens) return fail(LUMEN_ERR_INVALID, "params and tokens are required");
   if (bt->dtype != LUMEN_DTYPE_F32 && bt->dtype != LUMEN_DTYPE_BF16)
@@ -532,6 +567,18 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   }
   DeviceGuard g(s->device);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Arena arena;
+  lumen::RowWs* na_ws = nullptr;
+  if (noalloc) {
+    void* p = nullptr;
+    if (lumen::noalloc_scratch(&p) != hipSuccess) return fail(LUMEN_ERR_HIP, "noalloc: scratch address");
+    arena.base = static_cast<char*>(p);
+    // The row coordination blocks sit first, at the same place in every
+    // call: zero when the code object is loaded, and every launch leaves
+    // them zero (each row's last workgroup restores its block), so nothing
+    // is cleared per call.
+    na_ws = static_cast<lumen::RowWs*>(arena.take(sizeof(lumen::RowWs) * lumen::kNoAllocMaxRows));
+  }
 
   // rows, draws, penalty windows (host side)
   std::vector<RowParams> rows(B);
@@ -572,6 +619,19 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       // exactly one draw per sampled row (sampling.rs:1004)
       draws[b] = bt->rng_states ? lumen_xorshift64_next_f32(&bt->rng_states[b]) : bt->uniforms[b];
     }
+  }
+  if (V == 0 && noalloc) {
+    // sampling.rs:458-460: token 0, written by a kernel (no staging buffer)
+    DeviceGuard g0(s->device);
+    struct {
+      uint32_t* tokens;
+      uint32_t n;
+      uint32_t pad;
+    } za{bt->tokens, B, 0};
+    size_t zs = sizeof(za);
+    void* zc[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &za, HIP_LAUNCH_PARAM_BUFFER_SIZE, &zs, HIP_LAUNCH_PARAM_END};
+    return hip_fail(hipModuleLaunchKernel(s->fn_zero, (B + 255) / 256, 1, 1, 256, 1, 1, 0,
+                                          reinterpret_cast<hipStream_t>(stream), nullptr, zc));
   }
   if (V == 0) {
     // sampling.rs:458-460: empty logits sample token 0 and draw nothing.
@@ -626,7 +686,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     ka.debug_stop = stop;
   }
   uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
-  if (G > 1 && B >= 8 && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
+  if (G > 1 && B >= 8 && !noalloc && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
     const uint32_t nb = plan_blocks(rows, V, (uint32_t)s->max_resident, G, s->blk_map);
     if (nb) {
       nblocks = nb;
@@ -662,7 +722,26 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     ka.inline_draws = 1;
     for (uint32_t b = 0; b < B; ++b) ka.inline_uniforms[b] = draws[b];
   }
-  if (total > 0) {
+  if (total > 0 && noalloc) {
+    // the penalty counts of form A into the scratch array (inline rows and
+    // draws need nothing else); the copy reads pageable host memory, which
+    // HIP stages before hipMemcpyAsync returns
+    if (s->ids.size() > lumen::kNoAllocMaxCsr)
+      return fail(LUMEN_ERR_INVALID, "noalloc: more than 65536 form-A penalty entries");
+    s->img.assign(static_sz, 0);
+    std::memcpy(s->img.data() + off_offs, s->offs.data(), sizeof(uint32_t) * (B + 1));
+    if (!s->ids.empty()) {
+      std::memcpy(s->img.data() + off_ids, s->ids.data(), sizeof(uint32_t) * s->ids.size());
+      std::memcpy(s->img.data() + off_cnts, s->cnts.data(), sizeof(uint32_t) * s->cnts.size());
+    }
+    char* dp = static_cast<char*>(arena.take(static_sz));
+    if (!dp) return fail(LUMEN_ERR_INVALID, "noalloc: scratch too small");
+    if (hipMemcpyAsync(dp, s->img.data(), static_sz, hipMemcpyHostToDevice, st) != hipSuccess)
+      return fail(LUMEN_ERR_HIP, "staging copy");
+    ka.hist_off = reinterpret_cast<const uint32_t*>(dp + off_offs);
+    ka.hist_ids = reinterpret_cast<const uint32_t*>(dp + off_ids);
+    ka.hist_cnt = reinterpret_cast<const uint32_t*>(dp + off_cnts);
+  } else if (total > 0) {
     s->img.assign(static_sz, 0);
     if (!inl) std::memcpy(s->img.data(), rows.data(), sizeof(RowParams) * B);
     if (!s->blk_map.empty())
@@ -745,9 +824,14 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   }
   if (any_pen) {
     const uint64_t stride = ((uint64_t)V + 63) & ~uint64_t(63);
-    int rc = ensure_dev(s->pen_scratch, sizeof(float) * stride * B);
-    if (rc != LUMEN_OK) return rc;
-    ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
+    if (noalloc) {
+      ka.pen_scratch = static_cast<float*>(arena.take(sizeof(float) * stride * B));
+      if (!ka.pen_scratch) return fail(LUMEN_ERR_INVALID, "noalloc: scratch too small");
+    } else {
+      int rc = ensure_dev(s->pen_scratch, sizeof(float) * stride * B);
+      if (rc != LUMEN_OK) return rc;
+      ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
+    }
     ka.pen_stride = stride;
   }
   ka.tokens_mapped = tok_map;
@@ -755,6 +839,8 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   if (any_anti) {
     if (bt->guard_out) {
       ka.guard = bt->guard_out;
+    } else if (noalloc) {
+      return fail(LUMEN_ERR_INVALID, "noalloc: anti_restate rows need guard_out");
     } else {
       int rc = ensure_dev(s->guard, sizeof(uint32_t) * lumen::kGuardWords * B);
       if (rc != LUMEN_OK) return rc;
@@ -772,7 +858,13 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     hipError_t e = hipModuleLaunchKernel(s->fn_hist, B, 1, 1, 1024, 1, 1, 0, st, nullptr, hcfg);
     if (e != hipSuccess) return hip_fail(e);
   }
-  if (G > 1) {
+  if (G > 1 && noalloc) {
+    ka.ws = na_ws;
+    ka.cand = static_cast<uint64_t*>(arena.take(sizeof(uint64_t) * lumen::kCandStride * B));
+    ka.est = static_cast<uint32_t*>(arena.take(sizeof(uint32_t) * lumen::kRecWords * lumen::kRowRecs * B));
+    ka.hist = static_cast<float*>(arena.take(sizeof(float) * lumen::kMaxSlices * lumen::kMassBins * B));
+    if (!ka.ws || !ka.cand || !ka.est || !ka.hist) return fail(LUMEN_ERR_INVALID, "noalloc: scratch too small");
+  } else if (G > 1) {
     const size_t ws_bytes = sizeof(lumen::RowWs) * B;
     if (s->ws.cap < ws_bytes) {
       int rc = ensure_dev(s->ws, ws_bytes);

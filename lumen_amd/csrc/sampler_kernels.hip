@@ -3757,4 +3757,17 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
   }
   set_state(len);
 }
+// Token 0 for every row of an empty vocabulary (sampling.rs:458-460), for
+// the no-allocation entry point, which has no staging buffer to copy from.
+struct ZeroArgs {
+  uint32_t* tokens;
+  uint32_t n;
+  uint32_t pad;
+};
+
+extern "C" __global__ void __launch_bounds__(256) lumen_zero_tokens(ZeroArgs z) {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i < z.n) z.tokens[i] = 0u;
+}
+
 }  // namespace lumen

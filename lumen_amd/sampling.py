@@ -160,7 +160,8 @@ class Engine:
                      rngs: Optional[Sequence[Xorshift64]] = None,
                      penalty_counts=None, tokens_out=None, trace=None, penalized_out=None,
                      sync: bool = True, stream=None, uniforms_dev=None, rng_states_dev=None,
-                     hist_ring_dev=None, hist_len_dev=None, hist_epoch=0, guard_out=None, decoder=None):
+                     hist_ring_dev=None, hist_len_dev=None, hist_epoch=0, guard_out=None, decoder=None,
+                    noalloc: bool = False):
         """Samples every row of `logits` [B, V].
 
         histories: SamplerState.history per row (the window is applied here),
@@ -180,6 +181,8 @@ class Engine:
         candidates (required for anti_restate rows when sync=False);
         decoder: TokenBytes (or a list of bytes per id) for the guard's
         sub-word rule.
+        noalloc: use lumen_sampler_sample_batch_noalloc (asynchronous, at
+        most 8 rows; nothing allocated).
         Returns the token tensor (device); with sync=True also a host list.
         """
         import torch
@@ -257,7 +260,11 @@ class Engine:
         if penalized_out is not None:
             bt.penalized_out = penalized_out.data_ptr()
         s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
-        if sync:
+        if noalloc:
+            if sync:
+                raise ValueError("noalloc is asynchronous: pass sync=False")
+            rc = L.lumen_sampler_sample_batch_noalloc(self._h, ctypes.byref(bt), s)
+        elif sync:
             host = (ctypes.c_uint32 * B)()
             rc = L.lumen_sampler_sample_batch_sync(self._h, ctypes.byref(bt), host, s)
         else:
