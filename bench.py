@@ -196,7 +196,7 @@ def b1_decode_device_state(eng, draws=2_000):
 
     w = config2()
     dev = torch.from_numpy(w.logits).cuda()
-    ds = DeviceDecodeState(w.seeds, cap=8192, histories=w.histories)
+    ds = DeviceDecodeState(eng, w.seeds, cap=8192, histories=w.histories)
     tok = torch.empty(1, dtype=torch.int32, device=dev.device)
     times = []
     for i in range(draws + 50):
@@ -221,14 +221,14 @@ def b1_graph_decode(eng, per_graph=32, replays=20):
     w = config2()
     dev = torch.from_numpy(w.logits).cuda()
     tok = torch.empty(1, dtype=torch.int32, device=dev.device)
-    warm = DeviceDecodeState(w.seeds, cap=8192, histories=w.histories)
+    warm = DeviceDecodeState(eng, w.seeds, cap=8192, histories=w.histories)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         warm.step(eng, dev, w.params, tokens_out=tok, sync=False)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    ds = DeviceDecodeState(w.seeds, cap=8192, histories=w.histories)
+    ds = DeviceDecodeState(eng, w.seeds, cap=8192, histories=w.histories)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(per_graph):

@@ -188,6 +188,39 @@ typedef struct {
     const lumen_token_bytes *decoder;   /* host, or NULL (sub-word rule off) */
 } lumen_batch;
 
+/* Fresh-run initialisation of the device decode state: what
+ * decode_token_sampled does once per generation from GpuSamplerRunCfg
+ * (compute/mod.rs:202-227; engine.rs:340-371), the device form of
+ * `Xorshift64::new(seed)` plus the prompt recorded into SamplerState
+ * (sampling.rs:395-403, 381-384). */
+typedef struct lumen_decode_seed {
+    uint32_t batch;
+    /* The logits' vocabulary of the run's sample calls: whole-history
+     * windows keep counts for up to `vocab` distinct ids. */
+    uint32_t vocab;
+    /* [batch] the run's parameters, or NULL. When given, the penalty window
+     * of each penalized row is counted here from the prompt, so the first
+     * sample call finds its counts made (a prompt longer than hist_cap
+     * then works for a whole-history window, repeat_last_n 0). The sample
+     * calls must pass the same parameters, vocab, hist_cap and hist_epoch. */
+    const lumen_sampling_params *params;
+    const uint64_t *rng_seed_states;    /* host [batch]: Xorshift64::new(seed).state() */
+    /* host: row b's prompt is prompt_ids[prompt_offsets[b] .. prompt_offsets[b+1]]
+     * (GpuSamplerRunCfg.prompt_history); prompt_offsets NULL: empty prompts */
+    const uint64_t *prompt_offsets;
+    const uint32_t *prompt_ids;
+    uint64_t *rng_states_dev;           /* device [batch] out (lumen_batch.rng_states_dev), or NULL */
+    uint32_t *hist_ring_dev;            /* device [batch][hist_cap] out: the last hist_cap prompt ids */
+    uint32_t *hist_len_dev;             /* device [batch] out: prompt lengths */
+    uint32_t hist_cap;
+    uint32_t hist_epoch;
+} lumen_decode_seed;
+
+/* Writes the device decode state of lumen_decode_seed on `stream`
+ * (asynchronous; host inputs are staged before return). Not capturable:
+ * run it before capturing the decode step. */
+int lumen_sampler_decode_seed(lumen_sampler *s, const lumen_decode_seed *seed, lumen_stream stream);
+
 /* Context: loads the gfx950 code object on `device`. The code object is
  * embedded in the library; LUMEN_SAMPLER_CODE_OBJECT=<path> overrides it. */
 int lumen_sampler_create(lumen_sampler **out, int device);

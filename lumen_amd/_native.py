@@ -30,6 +30,7 @@ EXPORTS = (
     "lumen_sampler_sample_batch",
     "lumen_sampler_sample_batch_noalloc",
     "lumen_sampler_sample_batch_sync",
+    "lumen_sampler_decode_seed",
     "lumen_xorshift64_new",
     "lumen_xorshift64_next_u64",
     "lumen_xorshift64_next_f32",
@@ -115,6 +116,22 @@ class BatchC(ctypes.Structure):
     ]
 
 
+class DecodeSeedC(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_uint32),
+        ("vocab", ctypes.c_uint32),
+        ("params", ctypes.POINTER(SamplingParamsC)),
+        ("rng_seed_states", ctypes.POINTER(ctypes.c_uint64)),
+        ("prompt_offsets", ctypes.POINTER(ctypes.c_uint64)),
+        ("prompt_ids", ctypes.POINTER(ctypes.c_uint32)),
+        ("rng_states_dev", ctypes.c_void_p),
+        ("hist_ring_dev", ctypes.c_void_p),
+        ("hist_len_dev", ctypes.c_void_p),
+        ("hist_cap", ctypes.c_uint32),
+        ("hist_epoch", ctypes.c_uint32),
+    ]
+
+
 _lib = None
 
 
@@ -142,6 +159,9 @@ def load():
                                                   ctypes.POINTER(ctypes.c_uint32),
                                                   ctypes.c_void_p]
     L.lumen_xorshift64_new.restype = ctypes.c_uint64
+    L.lumen_sampler_decode_seed.restype = ctypes.c_int
+    L.lumen_sampler_decode_seed.argtypes = [ctypes.c_void_p, ctypes.POINTER(DecodeSeedC),
+                                            ctypes.c_void_p]
     L.lumen_xorshift64_new.argtypes = [ctypes.c_uint64]
     L.lumen_xorshift64_next_u64.restype = ctypes.c_uint64
     L.lumen_xorshift64_next_u64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]

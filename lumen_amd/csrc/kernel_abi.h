@@ -105,6 +105,15 @@ struct RowWs {
 constexpr int kGuardWords = 9;
 constexpr uint32_t kGuardNone = 0xffffffffu;
 
+// Arguments of lumen_zero_tokens (an empty vocabulary).
+struct ZeroArgs {
+  uint32_t* tokens;
+  uint32_t* ring;      // form C history ring, or NULL
+  uint32_t* ring_len;
+  uint32_t n;
+  uint32_t ring_cap;
+};
+
 struct KernelArgs {
   const void* logits;        // [B][row_stride] f32 or bf16, device
   uint64_t row_stride;       // elements
@@ -137,8 +146,8 @@ struct KernelArgs {
   const uint32_t* blk_map;
   uint32_t inline_rows;      // > 0: params come from inline_params
   uint32_t inline_draws;     // != 0: draws come from inline_uniforms
-  uint32_t debug_stop;       // development aid: split top-p rows stop after phase k (0: off)
-  uint32_t pad1;
+  uint32_t count_cap;        // form C: count entries per row (ring_cap, or vocab for long windows)
+  uint32_t pad2;
   // Synchronous calls: the token is also written to pinned host memory
   // mapped into the device, and *done_mapped (host memory) counts the rows
   // written, so the host waits on that count instead of a copy and a stream
@@ -152,15 +161,15 @@ struct KernelArgs {
   // Device history: a ring of the last ring_cap tokens of each row
   // ([B][ring_cap], token k of row b at k % ring_cap) and the count of tokens
   // recorded (ring_len[b]). lumen_hist_window builds the penalty window's
-  // counts from it into hist_off / hist_ids / hist_cnt (a region of ring_cap
-  // entries per row) and hist_end; the finisher of each row records its token.
+  // counts from it into hist_off / hist_ids / hist_cnt (a region of
+  // count_cap entries per row) and hist_end; the finisher of each row records its token.
   uint32_t* ring;
   uint32_t* ring_len;
   uint32_t* hist_end;        // [B] end of row b's counts (hist_off[b] = kHistBad on overflow)
   uint32_t ring_cap;
   uint32_t ring_epoch;       // lumen_batch.hist_epoch
   // [B][8] what row b's counts reflect: ring_len, window, ring address (lo,
-  // hi), ring_cap, ring_epoch. When the next call finds exactly one more token recorded
+  // hi), ring_cap, ring_epoch, count_cap. When the next call finds exactly one more token recorded
   // in the same ring with the same window, lumen_hist_window updates the
   // counts by that token (and the one leaving the window) instead of counting
   // the window again. ring_len 0xffffffff: nothing valid.

@@ -154,8 +154,8 @@ struct lumen_sampler {
   DevBuf guard;  // [B][kGuardWords] anti-restate candidates when the caller passes none
   uint32_t* guard_dev = nullptr;  // where the last call's candidates went
   bool any_anti = false;          // the last call had anti-restate rows
-  DevBuf wcnt;  // device history: [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts, [B][8] state
-  size_t wcnt_state_off = 0;  // word offset of the state in wcnt (layout of the last call)
+  DevBuf wcnt;  // device history: [B] offsets, [B] ends, [B][ccap] ids, [B][ccap] counts, [B][8] state
+  uint32_t wcnt_rows = 0, wcnt_ccap = 0;  // layout of the last call (rows, count capacity)
   int cu_count = 0;
   int max_resident = 0;  // workgroups of lumen_sample_rows resident at once
   hipEvent_t staged = nullptr;  // recorded after the last staging copy
@@ -198,8 +198,22 @@ struct DeviceGuard {
   }
 };
 
-int ensure_dev(DevBuf& b, size_t bytes) {
+// True while `st` is being captured into a graph. A call that would allocate,
+// clear or stage memory then refuses: those steps would be recorded into the
+// graph (and replayed) or are illegal under capture.
+bool capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) return false;
+  return cs != hipStreamCaptureStatusNone;
+}
+
+constexpr const char* kCaptureMsg =
+    "this call needs device set-up (a first call, a larger shape or a new history layout) "
+    "and cannot run under stream capture: make one eager call with the same shapes first";
+
+int ensure_dev(DevBuf& b, size_t bytes, hipStream_t st) {
   if (b.cap >= bytes) return LUMEN_OK;
+  if (capturing(st)) return fail(LUMEN_ERR_INVALID, kCaptureMsg);
   if (b.p) {
     if (hipDeviceSynchronize() != hipSuccess) return LUMEN_ERR_HIP;
     (void)hipFree(b.p);
@@ -209,6 +223,40 @@ int ensure_dev(DevBuf& b, size_t bytes) {
   size_t cap = std::max<size_t>(bytes, 4096);
   if (hipMalloc(&b.p, cap) != hipSuccess) return LUMEN_ERR_HIP;
   b.cap = cap;
+  return LUMEN_OK;
+}
+
+// Window counts of the device history (form C), in s->wcnt: [B] offsets,
+// [B] ends, [B][ccap] ids, [B][ccap] counts, [B][8] state. ccap is the ring
+// capacity, or the vocabulary when a penalized row counts its whole history
+// (repeat_last_n 0) or a window longer than the ring: such counts are kept up
+// to date token by token and can hold every distinct id.
+struct RingLayout {
+  uint32_t *off, *end, *ids, *cnt, *state;
+};
+
+int ring_layout(lumen_sampler* s, uint32_t B, uint32_t cap, uint32_t ccap, hipStream_t st,
+                RingLayout& L) {
+  const size_t state_off = 2 * (size_t)B + 2 * (size_t)ccap * B;
+  const size_t need = sizeof(uint32_t) * (state_off + 8 * (size_t)B);
+  const void* before = s->wcnt.p;
+  int rc = ensure_dev(s->wcnt, need, st);
+  if (rc != LUMEN_OK) return rc;
+  uint32_t* w = static_cast<uint32_t*>(s->wcnt.p);
+  if (s->wcnt.p != before || s->wcnt_rows != B || s->wcnt_ccap != ccap) {
+    if (capturing(st)) return fail(LUMEN_ERR_INVALID, kCaptureMsg);
+    // a new layout: nothing counted yet
+    if (hipMemsetAsync(w + state_off, 0xff, sizeof(uint32_t) * 8 * (size_t)B, st) != hipSuccess)
+      return fail(LUMEN_ERR_HIP, "window-count state init");
+    s->wcnt_rows = B;
+    s->wcnt_ccap = ccap;
+  }
+  (void)cap;
+  L.off = w;
+  L.end = w + B;
+  L.ids = w + 2 * (size_t)B;
+  L.cnt = w + 2 * (size_t)B + (size_t)ccap * B;
+  L.state = w + state_off;
   return LUMEN_OK;
 }
 
@@ -620,41 +668,22 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       draws[b] = bt->rng_states ? lumen_xorshift64_next_f32(&bt->rng_states[b]) : bt->uniforms[b];
     }
   }
-  if (V == 0 && noalloc) {
-    // sampling.rs:458-460: token 0, written by a kernel (no staging buffer)
-    DeviceGuard g0(s->device);
-    struct {
-      uint32_t* tokens;
-      uint32_t n;
-      uint32_t pad;
-    } za{bt->tokens, B, 0};
+  if (V == 0) {
+    // sampling.rs:458-460: empty logits sample token 0 and draw nothing;
+    // Sampler::sample records it (sampling.rs:429-433), so in form C the
+    // kernel also appends 0 to each row's ring. A kernel (no staging copy,
+    // no memset node) keeps the call capturable and allocation-free.
+    s->any_anti = false;
+    lumen::ZeroArgs za{};
+    za.tokens = bt->tokens;
+    za.n = B;
+    za.ring = bt->hist_ring_dev;
+    za.ring_len = bt->hist_len_dev;
+    za.ring_cap = bt->hist_cap;
     size_t zs = sizeof(za);
     void* zc[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &za, HIP_LAUNCH_PARAM_BUFFER_SIZE, &zs, HIP_LAUNCH_PARAM_END};
     return hip_fail(hipModuleLaunchKernel(s->fn_zero, (B + 255) / 256, 1, 1, 256, 1, 1, 0,
                                           reinterpret_cast<hipStream_t>(stream), nullptr, zc));
-  }
-  if (V == 0) {
-    // sampling.rs:458-460: empty logits sample token 0 and draw nothing.
-    // Written with a copy (not a memset node) so the call stays capturable.
-    if (s->staged_pending) {
-      if (hipEventSynchronize(s->staged) != hipSuccess) return LUMEN_ERR_HIP;
-      s->staged_pending = false;
-    }
-    const size_t bytes = sizeof(uint32_t) * B;
-    if (s->pin_cap < bytes) {
-      if (s->pin) (void)hipHostFree(s->pin);
-      s->pin = nullptr;
-      s->pin_cap = 0;
-      size_t cap = std::max<size_t>(bytes, 65536);
-      if (hipHostMalloc(&s->pin, cap, hipHostMallocDefault) != hipSuccess) return LUMEN_ERR_HIP;
-      s->pin_cap = cap;
-    }
-    std::memset(s->pin, 0, bytes);
-    if (hipMemcpyAsync(bt->tokens, s->pin, bytes, hipMemcpyHostToDevice, st) != hipSuccess)
-      return LUMEN_ERR_HIP;
-    if (hipEventRecord(s->staged, st) != hipSuccess) return LUMEN_ERR_HIP;
-    s->staged_pending = true;
-    return LUMEN_OK;
   }
 
   KernelArgs ka;
@@ -677,14 +706,6 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
                                                   (uint32_t)s->max_resident / padded));
   ka.slices = G;
   ka.xcd_rows = (B >= 8 && G > 1) ? 1u : 0u;
-  {
-    // development aid (phase costs on the critical path): LUMEN_SAMPLER_DEBUG_STOP=k
-    static const uint32_t stop = [] {
-      const char* e = std::getenv("LUMEN_SAMPLER_DEBUG_STOP");
-      return e ? (uint32_t)std::strtoul(e, nullptr, 10) : 0u;
-    }();
-    ka.debug_stop = stop;
-  }
   uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
   if (G > 1 && B >= 8 && !noalloc && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
     const uint32_t nb = plan_blocks(rows, V, (uint32_t)s->max_resident, G, s->blk_map);
@@ -754,11 +775,12 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       }
     }
     const size_t dev_cap_before = s->stage.cap;
-    int rc = ensure_dev(s->stage, total);
+    int rc = ensure_dev(s->stage, total, st);
     if (rc != LUMEN_OK) return rc;
     if (s->stage.cap != dev_cap_before) s->last_img.clear();  // new device buffer
     const bool copy_static = static_sz > 0 && s->img != s->last_img;
     if (copy_static || draw_block) {
+      if (capturing(st)) return fail(LUMEN_ERR_INVALID, kCaptureMsg);
       if (s->staged_pending) {
         if (hipEventSynchronize(s->staged) != hipSuccess) return fail(LUMEN_ERR_HIP, "staging wait");
         s->staged_pending = false;
@@ -794,25 +816,19 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     }
   }
   if (ring) {
-    const size_t cap = bt->hist_cap;
-    // [B] offsets, [B] ends, [B][cap] ids, [B][cap] counts, [kMaxStateRows][8] state
-    const size_t state_off = 2 * B + 2 * cap * B;
-    const size_t need = sizeof(uint32_t) * (state_off + 8 * (size_t)B);
-    const void* before = s->wcnt.p;
-    int rc = ensure_dev(s->wcnt, need);
+    uint32_t ccap = bt->hist_cap;
+    for (uint32_t b = 0; b < B; ++b)
+      if ((rows[b].flags & lumen::kPen) && (rows[b].window == 0u || rows[b].window > bt->hist_cap))
+        ccap = std::max<uint32_t>(ccap, V);
+    RingLayout L;
+    int rc = ring_layout(s, B, bt->hist_cap, ccap, st, L);
     if (rc != LUMEN_OK) return rc;
-    uint32_t* w = static_cast<uint32_t*>(s->wcnt.p);
-    if (s->wcnt.p != before || s->wcnt_state_off != state_off) {
-      // a new layout: nothing counted yet
-      if (hipMemsetAsync(w + state_off, 0xff, sizeof(uint32_t) * 8 * (size_t)B, st) != hipSuccess)
-        return fail(LUMEN_ERR_HIP, "window-count state init");
-      s->wcnt_state_off = state_off;
-    }
-    ka.hist_state = w + state_off;
-    ka.hist_off = w;
-    ka.hist_end = w + B;
-    ka.hist_ids = w + 2 * B;
-    ka.hist_cnt = w + 2 * B + cap * B;
+    ka.hist_state = L.state;
+    ka.hist_off = L.off;
+    ka.hist_end = L.end;
+    ka.hist_ids = L.ids;
+    ka.hist_cnt = L.cnt;
+    ka.count_cap = ccap;
     ka.ring = bt->hist_ring_dev;
     ka.ring_len = bt->hist_len_dev;
     ka.ring_cap = bt->hist_cap;
@@ -828,7 +844,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       ka.pen_scratch = static_cast<float*>(arena.take(sizeof(float) * stride * B));
       if (!ka.pen_scratch) return fail(LUMEN_ERR_INVALID, "noalloc: scratch too small");
     } else {
-      int rc = ensure_dev(s->pen_scratch, sizeof(float) * stride * B);
+      int rc = ensure_dev(s->pen_scratch, sizeof(float) * stride * B, st);
       if (rc != LUMEN_OK) return rc;
       ka.pen_scratch = static_cast<float*>(s->pen_scratch.p);
     }
@@ -842,7 +858,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     } else if (noalloc) {
       return fail(LUMEN_ERR_INVALID, "noalloc: anti_restate rows need guard_out");
     } else {
-      int rc = ensure_dev(s->guard, sizeof(uint32_t) * lumen::kGuardWords * B);
+      int rc = ensure_dev(s->guard, sizeof(uint32_t) * lumen::kGuardWords * B, st);
       if (rc != LUMEN_OK) return rc;
       ka.guard = static_cast<uint32_t*>(s->guard.p);
     }
@@ -867,19 +883,19 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   } else if (G > 1) {
     const size_t ws_bytes = sizeof(lumen::RowWs) * B;
     if (s->ws.cap < ws_bytes) {
-      int rc = ensure_dev(s->ws, ws_bytes);
+      int rc = ensure_dev(s->ws, ws_bytes, st);
       if (rc != LUMEN_OK) return rc;
       // zero once at allocation; afterwards each launch leaves it zeroed
       if (hipMemset(s->ws.p, 0, s->ws.cap) != hipSuccess) return fail(LUMEN_ERR_HIP, "workspace init");
     }
-    int rc = ensure_dev(s->cand, sizeof(uint64_t) * lumen::kCandStride * B);
+    int rc = ensure_dev(s->cand, sizeof(uint64_t) * lumen::kCandStride * B, st);
     if (rc != LUMEN_OK) return rc;
-    rc = ensure_dev(s->est, sizeof(uint32_t) * lumen::kRecWords * lumen::kRowRecs * B);
+    rc = ensure_dev(s->est, sizeof(uint32_t) * lumen::kRecWords * lumen::kRowRecs * B, st);
     if (rc != LUMEN_OK) return rc;
     ka.ws = static_cast<lumen::RowWs*>(s->ws.p);
     ka.cand = static_cast<uint64_t*>(s->cand.p);
     ka.est = static_cast<uint32_t*>(s->est.p);
-    rc = ensure_dev(s->hist, sizeof(float) * lumen::kMaxSlices * lumen::kMassBins * B);
+    rc = ensure_dev(s->hist, sizeof(float) * lumen::kMaxSlices * lumen::kMassBins * B, st);
     if (rc != LUMEN_OK) return rc;
     ka.hist = static_cast<float*>(s->hist.p);
     // Every wait inside the kernel is bounded and reports a row failure on
@@ -900,6 +916,124 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   return hip_fail(e);
 }
 }  // namespace
+
+int lumen_sampler_decode_seed(lumen_sampler* s, const lumen_decode_seed* d, lumen_stream stream) {
+  if (!s || !d) return fail(LUMEN_ERR_INVALID, "null context or seed");
+  const uint32_t B = d->batch, cap = d->hist_cap;
+  if (B == 0) return LUMEN_OK;
+  if (!d->hist_ring_dev || !d->hist_len_dev) return fail(LUMEN_ERR_INVALID, "hist_ring_dev and hist_len_dev are required");
+  if (cap == 0 || cap > lumen::kRingMaxCap) return fail(LUMEN_ERR_INVALID, "hist_cap must be between 1 and 8192");
+  if (d->rng_states_dev && !d->rng_seed_states) return fail(LUMEN_ERR_INVALID, "rng_states_dev needs rng_seed_states");
+  if (d->prompt_offsets && !d->prompt_ids && d->prompt_offsets[B] > d->prompt_offsets[0])
+    return fail(LUMEN_ERR_INVALID, "prompt_offsets without prompt_ids");
+  DeviceGuard g(s->device);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (capturing(st)) return fail(LUMEN_ERR_INVALID, "lumen_sampler_decode_seed cannot run under stream capture");
+  auto prompt = [&](uint32_t b, const uint32_t** p, uint64_t* n) {
+    *p = nullptr;
+    *n = 0;
+    if (!d->prompt_offsets) return true;
+    const uint64_t h0 = d->prompt_offsets[b], h1 = d->prompt_offsets[b + 1];
+    if (h1 < h0 || h1 - h0 > 0xfffffffeull) return false;
+    *p = d->prompt_ids + h0;
+    *n = h1 - h0;
+    return true;
+  };
+  // host image: [B] u64 states | [B] lens | [B][cap] ring | window counts
+  std::vector<uint32_t> lens(B), ring((size_t)B * cap, 0u);
+  for (uint32_t b = 0; b < B; ++b) {
+    const uint32_t* p;
+    uint64_t n;
+    if (!prompt(b, &p, &n)) return fail(LUMEN_ERR_INVALID, "prompt_offsets must be non-decreasing");
+    lens[b] = (uint32_t)n;
+    for (uint64_t k = n > cap ? n - cap : 0; k < n; ++k) ring[(size_t)b * cap + k % cap] = p[k];
+  }
+  // window counts (form A's counting, sampling.rs:860-878), with the state
+  // words lumen_hist_window keeps: counts made at ring_len = prompt length
+  RingLayout L{};
+  uint32_t ccap = cap;
+  std::vector<RowParams> rows(B);
+  std::vector<uint32_t> head;  // [B] offsets, [B] ends, [B][8] state
+  std::vector<uint32_t> rstart(B + 1, 0);
+  s->ids.clear();
+  s->cnts.clear();
+  if (d->params) {
+    for (uint32_t b = 0; b < B; ++b) {
+      resolve_row(d->params[b], d->vocab, true, rows[b]);
+      if ((rows[b].flags & lumen::kPen) && (rows[b].window == 0u || rows[b].window > cap))
+        ccap = std::max<uint32_t>(ccap, d->vocab);
+    }
+    head.assign(2 * (size_t)B + 8 * (size_t)B, 0xffffffffu);
+    const uint64_t rid = (uint64_t)(uintptr_t)d->hist_ring_dev;
+    for (uint32_t b = 0; b < B; ++b) {
+      const uint32_t base = b * ccap;
+      head[b] = base;
+      head[B + b] = base;
+      if (rows[b].flags & lumen::kPen) {
+        const uint32_t* p;
+        uint64_t n;
+        (void)prompt(b, &p, &n);
+        const size_t k0 = s->ids.size();
+        if (n > 0) count_window(s, p, n, rows[b].window);
+        const size_t k = s->ids.size() - k0;
+        if (k > ccap) return fail(LUMEN_ERR_INVALID, "prompt ids outside the vocabulary");
+        head[B + b] = base + (uint32_t)k;
+        uint32_t* sw = &head[2 * (size_t)B + 8 * (size_t)b];
+        sw[0] = (uint32_t)n;
+        sw[1] = rows[b].window;
+        sw[2] = (uint32_t)rid;
+        sw[3] = (uint32_t)(rid >> 32);
+        sw[4] = cap;
+        sw[5] = d->hist_epoch;
+        sw[6] = ccap;
+        sw[7] = 0;
+      }
+      rstart[b + 1] = (uint32_t)s->ids.size();
+    }
+    int rc = ring_layout(s, B, cap, ccap, st, L);
+    if (rc != LUMEN_OK) return rc;
+  }
+  const size_t n_ids = s->ids.size();
+  const size_t bytes = sizeof(uint64_t) * B + sizeof(uint32_t) * (B + ring.size() + head.size() + 2 * n_ids);
+  if (s->staged_pending) {
+    if (hipEventSynchronize(s->staged) != hipSuccess) return fail(LUMEN_ERR_HIP, "staging wait");
+    s->staged_pending = false;
+  }
+  if (s->pin_cap < bytes) {
+    if (s->pin) (void)hipHostFree(s->pin);
+    s->pin = nullptr;
+    s->pin_cap = 0;
+    const size_t c = std::max<size_t>(bytes, 65536);
+    if (hipHostMalloc(&s->pin, c, hipHostMallocDefault) != hipSuccess)
+      return fail(LUMEN_ERR_HIP, "pinned staging allocation");
+    s->pin_cap = c;
+  }
+  char* hp = static_cast<char*>(s->pin);
+  auto put = [&](void* dst, const void* src, size_t n) -> bool {
+    if (n == 0) return true;
+    std::memcpy(hp, src, n);
+    const bool ok = hipMemcpyAsync(dst, hp, n, hipMemcpyHostToDevice, st) == hipSuccess;
+    hp += n;
+    return ok;
+  };
+  bool ok = true;
+  if (d->rng_states_dev) ok &= put(d->rng_states_dev, d->rng_seed_states, sizeof(uint64_t) * B);
+  ok &= put(d->hist_len_dev, lens.data(), sizeof(uint32_t) * B);
+  ok &= put(d->hist_ring_dev, ring.data(), sizeof(uint32_t) * ring.size());
+  if (d->params) {
+    ok &= put(L.off, head.data(), sizeof(uint32_t) * 2 * B);
+    ok &= put(L.state, head.data() + 2 * B, sizeof(uint32_t) * 8 * B);
+    for (uint32_t b = 0; b < B; ++b) {
+      const size_t k0 = rstart[b], k = rstart[b + 1] - k0;
+      ok &= put(L.ids + (size_t)b * ccap, s->ids.data() + k0, sizeof(uint32_t) * k);
+      ok &= put(L.cnt + (size_t)b * ccap, s->cnts.data() + k0, sizeof(uint32_t) * k);
+    }
+  }
+  if (!ok) return fail(LUMEN_ERR_HIP, "seed copy");
+  if (hipEventRecord(s->staged, st) != hipSuccess) return fail(LUMEN_ERR_HIP, "event record");
+  s->staged_pending = true;
+  return LUMEN_OK;
+}
 
 int lumen_sampler_sample_batch_sync(lumen_sampler* s, const lumen_batch* bt, uint32_t* tokens_host,
                                     lumen_stream stream) {

@@ -34,6 +34,15 @@
 #include "expf_glibc.h"
 #include "kernel_abi.h"
 
+// Development aid: -DLUMEN_DEBUG_STOP=k (only in development code objects)
+// makes the split top-p and top-k rows stop after phase k to price each
+// phase on the critical path. Release builds compile every check away.
+#ifdef LUMEN_DEBUG_STOP
+#define kDebugStop ((uint32_t)(LUMEN_DEBUG_STOP))
+#else
+#define kDebugStop 0u
+#endif
+
 // Development aid: -DLUMEN_TIMING records phase timestamps (100 MHz wall
 // clock) in thread 0 of the finishing workgroup of row 0 and prints them
 // once when that row's result is written.
@@ -1373,7 +1382,7 @@ __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const Row
     nlist = nk;
   }
   LUMEN_TICK("small_before_final", b);
-  if ((a.debug_stop >> 8) == 6u && !(P.flags & kTopP && tr.path == 4u)) {
+  if ((kDebugStop >> 8) == 6u && !(P.flags & kTopP && tr.path == 4u)) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -2697,7 +2706,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   LUMEN_TICK("topk_start", b);
-  if ((a.debug_stop >> 8) == 15u) return;
+  if ((kDebugStop >> 8) == 15u) return;
   uint32_t tau;
   const uint32_t* bm;
   if (k <= (uint32_t)kThreads && sc_len_max(V, G) <= 16u * kThreads) {
@@ -2705,12 +2714,12 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
     tau = topk_collect16(row, sc, bm, k, s);
     LUMEN_TICK("topk_sampled", b);
-    if ((a.debug_stop >> 8) == 1u) return;
+    if ((kDebugStop >> 8) == 1u) return;
   } else {
     const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
     tau = sample_threshold(row, V, target, s);
     LUMEN_TICK("topk_sampled", b);
-    if ((a.debug_stop >> 8) == 1u) return;
+    if ((kDebugStop >> 8) == 1u) return;
     bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
     if (threadIdx.x == 0) s.cnt = 0;
     __syncthreads();
@@ -2738,7 +2747,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   }
   flush_candidates(cand, &ws.cand_n, s);
   LUMEN_TICK("topk_compacted", b);
-  if ((a.debug_stop >> 8) == 2u) return;
+  if ((kDebugStop >> 8) == 2u) return;
   const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
   if (old != G - 1u) return;
   LUMEN_TICK("topk_finisher", b);
@@ -2753,7 +2762,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) s.A[j] = cand[j];
   __syncthreads();
   LUMEN_TICK("topk_loaded", b);
-  if ((a.debug_stop >> 8) == 3u) {
+  if ((kDebugStop >> 8) == 3u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -2793,7 +2802,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     ns = s.cnt;
   }
   LUMEN_TICK("topk_sort1", b);
-  if ((a.debug_stop >> 8) == 4u) {
+  if ((kDebugStop >> 8) == 4u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -2803,7 +2812,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   tr.topk_cutoff_key = cut;
   tr.topk_survivors = ns;
   LUMEN_TICK("topk_sorted", b);
-  if ((a.debug_stop >> 8) == 5u) {
+  if ((kDebugStop >> 8) == 5u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3257,10 +3266,10 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
   LUMEN_TICK("p_start", b);
-  if ((a.debug_stop & 255u) == 15u) return;
+  if ((kDebugStop & 255u) == 15u) return;
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
   LUMEN_TICK("p_sampled", b);
-  if ((a.debug_stop & 255u) == 1u) return;
+  if ((kDebugStop & 255u) == 1u) return;
   const float tv = tau ? key2f(tau) : kNegInf;
   const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
   float mt = kNegInf;
@@ -3295,13 +3304,13 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     ws.part_e[sl] = es_tot;
   }
   LUMEN_TICK("p_pass1", b);
-  if ((a.debug_stop & 255u) == 2u) return;
+  if ((kDebugStop & 255u) == 2u) return;
   wg_arrive(&ws.bar, 0xffffffffu, s);
   const bool ok = wg_wait_geq(&ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("p_barrier", b);
-  if ((a.debug_stop & 255u) == 3u) return;
+  if ((kDebugStop & 255u) == 3u) return;
   float m1 = kNegInf;
   uint32_t anynan = 0;
   double p_slice = 0.0;
@@ -3323,7 +3332,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     else chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
   }
   LUMEN_TICK("p_prepared", b);
-  if ((a.debug_stop & 255u) == 4u) return;
+  if ((kDebugStop & 255u) == 4u) return;
   if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) {
     LUMEN_TICK("p_not_finisher", b);
     LUMEN_TICK_DUMP(b);
@@ -3370,7 +3379,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     __syncthreads();
   }
   LUMEN_TICK("p_gathered", b);
-  if ((a.debug_stop & 255u) == 5u) {
+  if ((kDebugStop & 255u) == 5u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3378,7 +3387,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const float S1 = m16 ? chain_walk<16>(a, b, G, row, m1, &nre, s)
                        : chain_walk<32>(a, b, G, row, m1, &nre, s);
   LUMEN_TICK("p_chain", b);
-  if ((a.debug_stop & 255u) == 6u) {
+  if ((kDebugStop & 255u) == 6u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3455,7 +3464,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   const uint32_t n = s.cnt;
   LUMEN_TICK("p_window_built", b);
-  if ((a.debug_stop & 255u) == 7u) {
+  if ((kDebugStop & 255u) == 7u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3467,7 +3476,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
     sort_u64_asc(s.Bk, n, s.A, s, hint);
   }
   LUMEN_TICK("p_window_sorted", b);
-  if ((a.debug_stop & 255u) == 8u) {
+  if ((kDebugStop & 255u) == 8u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3479,7 +3488,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   EcssResult wk = list_ecss(n, [&](uint32_t j) { return ps[pad16(j)]; }, kEcssFindGe, P.top_p, 0.f, s);
   LUMEN_TICK(s.est.fail == 2 ? "p_walk_nofit" : s.est.fail ? "p_walk_failed" : "p_walk_ok", b);
-  if ((a.debug_stop & 255u) == 9u) {
+  if ((kDebugStop & 255u) == 9u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3498,7 +3507,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   sort_u64_asc(s.A, nk, s.Bk, s, ((uint64_t)span_mask(a.vocab) << 32) | 0xffffffffull);
   LUMEN_TICK("p_kept_sorted", b);
-  if ((a.debug_stop & 255u) == 10u) {
+  if ((kDebugStop & 255u) == 10u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
@@ -3612,10 +3621,13 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
 // window is 0, counted per distinct id). Runs before lumen_sample_rows on the
 // same stream. Counts go through an LDS hash table (2 * kRingMaxCap slots,
 // linear probing), then out as (id, count) pairs in slot order, which the
-// sampler does not depend on. A window longer than the ring cannot be
-// counted: hist_off[b] = kHistBad (an empty range, since hist_end[b] is
-// below it) and the row's token becomes LUMEN_TOKEN_ERROR with
-// kStatusHistOverflow when it is written.
+// sampler does not depend on. Counts that follow the history token by token
+// (one token recorded since they were made) are updated in place instead,
+// which also carries a whole-history window (or any window from which
+// nothing leaves) past the ring's capacity. A window that must be counted
+// again but is longer than the ring cannot be: hist_off[b] = kHistBad (an
+// empty range, since hist_end[b] is below it) and the row's token becomes
+// LUMEN_TOKEN_ERROR with kStatusHistOverflow when it is written.
 constexpr uint32_t kHashSlots = 2u * kRingMaxCap;
 constexpr uint32_t kHashEmpty = 0xffffffffu;
 static_assert(kHashSlots == (1u << 14), "the hash takes the top 14 bits");
@@ -3631,8 +3643,9 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
   const uint32_t b = blockIdx.x, t = threadIdx.x;
   if (b >= a.batch) return;
   const RowParams& P = a.inline_rows ? a.inline_params[b] : a.params[b];
-  const uint32_t cap = a.ring_cap;
-  const uint32_t base = b * cap;
+  const uint32_t cap = a.ring_cap, ccap = a.count_cap;
+  const uint64_t rbase = (uint64_t)b * cap;   // the row's ring
+  const uint32_t base = b * ccap;             // the row's counts
   uint32_t* off = const_cast<uint32_t*>(a.hist_off);
   uint32_t* ids = const_cast<uint32_t*>(a.hist_ids);
   uint32_t* cnt = const_cast<uint32_t*>(a.hist_cnt);
@@ -3648,6 +3661,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
       st[3] = (uint32_t)(rid >> 32);
       st[4] = cap;
       st[5] = a.ring_epoch;
+      st[6] = ccap;
     }
   };
   if (!(P.flags & kPen) || w == 0u) {
@@ -3658,24 +3672,21 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
     set_state((P.flags & kPen) ? len : 0xffffffffu);
     return;
   }
-  if (w > cap) {
-    // no counts (an empty range); the row's finisher reports the overflow
-    if (t == 0) {
-      off[b] = kHistBad;
-      a.hist_end[b] = base;
-    }
-    set_state(0xffffffffu);
-    return;
-  }
-  const bool follows = st[0] != 0xffffffffu && st[0] + 1u == len && st[1] == P.window &&
-                       st[2] == (uint32_t)rid && st[3] == (uint32_t)(rid >> 32) && st[4] == cap && st[5] == a.ring_epoch &&
-                       off[b] == base;
+  // the counts were made for this ring, window and layout
+  const bool same = st[0] != 0xffffffffu && st[1] == P.window && st[2] == (uint32_t)rid &&
+                    st[3] == (uint32_t)(rid >> 32) && st[4] == cap && st[5] == a.ring_epoch &&
+                    st[6] == ccap && off[b] == base;
+  // ... and already reflect this history (seeded, or nothing recorded since)
+  if (same && st[0] == len) return;
+  // A token that leaves the window sits at len - 1 - window; the ring still
+  // holds it (the new token has not overwritten it) only when window < cap.
+  const bool leaves = P.window > 0u && len - 1u >= P.window;
+  const bool follows = same && st[0] + 1u == len && (!leaves || P.window < cap);
   if (follows) {
     // one token recorded since the counts were made (by the sampler): add
     // it, and take out the token that left a full window
-    const uint32_t* ring = a.ring + (uint64_t)base;
+    const uint32_t* ring = a.ring + rbase;
     const uint32_t tin = ring[(len - 1u) % cap];
-    const bool leaves = P.window > 0u && len - 1u >= P.window;
     const uint32_t tout = leaves ? ring[(len - 1u - P.window) % cap] : kHashEmpty;
     const uint32_t n0 = a.hist_end[b] - base;
     if (t == 0) {
@@ -3691,7 +3702,8 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
       }
     __syncthreads();
     const uint32_t pin = nout, pout = pout_s;
-    if (!(tin != tout && leaves && pout == kHashEmpty)) {
+    const bool grows = tin != tout && pin == kHashEmpty;
+    if (!(tin != tout && leaves && pout == kHashEmpty) && !(grows && n0 >= ccap)) {
       if (t == 0) {
         uint32_t n = n0;
         if (tin != tout) {
@@ -3723,13 +3735,23 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
     // the counts do not hold the leaving token: count the window again
     __syncthreads();
   }
+  if (w > cap) {
+    // the ring no longer holds the window: no counts (an empty range); the
+    // row's finisher reports the overflow
+    if (t == 0) {
+      off[b] = kHistBad;
+      a.hist_end[b] = base;
+    }
+    set_state(0xffffffffu);
+    return;
+  }
   for (uint32_t i = t; i < kHashSlots; i += blockDim.x) {
     hkey[i] = kHashEmpty;
     hcnt[i] = 0u;
   }
   if (t == 0) nout = 0u;
   __syncthreads();
-  const uint32_t* ring = a.ring + (uint64_t)base;
+  const uint32_t* ring = a.ring + rbase;
   for (uint32_t j = t; j < w; j += blockDim.x) {
     const uint32_t id = ring[(len - w + j) % cap];
     uint32_t h = (id * 2654435761u) >> (32 - 14);  // Fibonacci hashing into 2^14 slots
@@ -3757,17 +3779,18 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_hist_window(KernelArgs 
   }
   set_state(len);
 }
-// Token 0 for every row of an empty vocabulary (sampling.rs:458-460), for
-// the no-allocation entry point, which has no staging buffer to copy from.
-struct ZeroArgs {
-  uint32_t* tokens;
-  uint32_t n;
-  uint32_t pad;
-};
-
+// Token 0 for every row of an empty vocabulary (sampling.rs:458-460),
+// recorded into the row's device history ring when there is one
+// (SamplerState::record, sampling.rs:381-384).
 extern "C" __global__ void __launch_bounds__(256) lumen_zero_tokens(ZeroArgs z) {
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  if (i < z.n) z.tokens[i] = 0u;
+  if (i >= z.n) return;
+  z.tokens[i] = 0u;
+  if (z.ring) {
+    const uint32_t n = z.ring_len[i];
+    z.ring[(uint64_t)i * z.ring_cap + n % z.ring_cap] = 0u;
+    z.ring_len[i] = n + 1u;
+  }
 }
 
 }  // namespace lumen

@@ -101,6 +101,9 @@ class SamplerState:
 
     history: List[int] = field(default_factory=list)
     freq: Dict[int, int] = field(default_factory=dict)
+    # the embedder's byte decoder (SamplerState::decoder): a TokenBytes, a
+    # list of bytes per id, or None (the anti-restate sub-word rule is off)
+    decoder: Optional[object] = None
 
     def record(self, token: int):
         self.history.append(int(token))
@@ -315,30 +318,53 @@ def next_epoch() -> int:
 class DeviceDecodeState:
     """Per-row decode state kept in device memory: the Xorshift64 state
     (Sampler::rng, sampling.rs:395-403) and the history ring
-    (SamplerState::history, sampling.rs:353-389) of `cap` tokens. A decode
-    step samples with `step(engine, logits, params)`: no host draw, no
-    history upload, and the sampled tokens are recorded on the device.
-    Writing `ring` or `lens` directly (a new prompt) must be followed by
-    `self.epoch = next_epoch()`, so the window counts are made again."""
+    (SamplerState::history, sampling.rs:353-389) of `cap` tokens. It is
+    seeded through lumen_sampler_decode_seed from the seeds and the prompts
+    (GpuSamplerRunCfg.rng_seed_state / prompt_history, compute/mod.rs:202-227);
+    with `params` and `vocab` the prompts' penalty windows are counted there
+    too. A decode step samples with `step(engine, logits, params)`: no host
+    draw, no history upload, and the sampled tokens are recorded on the
+    device. Writing `ring` or `lens` directly (a new prompt) must be followed
+    by `self.epoch = next_epoch()`, so the window counts are made again."""
 
-    def __init__(self, seeds: Sequence[int], cap: int = 4096, device: int = 0,
-                 histories: Optional[Sequence[Sequence[int]]] = None):
+    def __init__(self, eng: "Engine", seeds: Sequence[int], cap: int = 4096,
+                 histories: Optional[Sequence[Sequence[int]]] = None,
+                 params: Optional[Sequence[SamplingParams]] = None, vocab: int = 0,
+                 stream=None):
         import torch
 
         B = len(seeds)
-        dev = torch.device("cuda", device)
-        st = np.array([Xorshift64(s).state() for s in seeds], dtype=np.uint64)
-        self.rng = torch.from_numpy(st.view(np.int64).copy()).to(dev)
-        ring = np.zeros((B, cap), dtype=np.uint32)
-        lens = np.zeros(B, dtype=np.uint32)
-        for b, h in enumerate(histories or []):
-            h = np.asarray(h, dtype=np.uint32).reshape(-1)
-            for k, tok in enumerate(h):
-                ring[b, k % cap] = tok
-            lens[b] = h.size
-        self.ring = torch.from_numpy(ring.view(np.int32)).to(dev)
-        self.lens = torch.from_numpy(lens.view(np.int32)).to(dev)
+        dev = torch.device("cuda", eng.device)
+        self.rng = torch.empty(B, dtype=torch.int64, device=dev)
+        self.ring = torch.empty((B, cap), dtype=torch.int32, device=dev)
+        self.lens = torch.empty(B, dtype=torch.int32, device=dev)
         self.epoch = next(_epochs)
+        st = np.array([Xorshift64(s).state() for s in seeds], dtype=np.uint64)
+        hs = [np.asarray(h, dtype=np.uint32).reshape(-1) for h in (histories or [])]
+        hs += [np.zeros(0, dtype=np.uint32)] * (B - len(hs))
+        offs = np.zeros(B + 1, dtype=np.uint64)
+        offs[1:] = np.cumsum([h.size for h in hs])
+        ids = np.concatenate(hs + [np.zeros(1, dtype=np.uint32)])
+        d = _native.DecodeSeedC()
+        d.batch = B
+        d.vocab = int(vocab)
+        keep = [st, offs, ids]
+        if params is not None:
+            pc = (_native.SamplingParamsC * B)(*[p.to_c() for p in params])
+            keep.append(pc)
+            d.params = pc
+        d.rng_seed_states = st.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
+        d.prompt_offsets = offs.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
+        d.prompt_ids = ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+        d.rng_states_dev = self.rng.data_ptr()
+        d.hist_ring_dev = self.ring.data_ptr()
+        d.hist_len_dev = self.lens.data_ptr()
+        d.hist_cap = cap
+        d.hist_epoch = self.epoch
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        rc = _native.load().lumen_sampler_decode_seed(eng._h, ctypes.byref(d), s)
+        _native.check(rc, "lumen_sampler_decode_seed")
+        del keep  # staged into pinned memory before the call returned
 
     def step(self, eng: "Engine", logits, params: Sequence[SamplingParams], **kw):
         return eng.sample_batch(logits, params, rng_states_dev=self.rng,
@@ -433,7 +459,8 @@ def sample_logits(logits, params: SamplingParams, state: SamplerState, rng: Xors
     dev = logits.device.index or 0
     if logits.numel() == 0:
         return 0
-    _, toks = engine(dev).sample_batch(logits, [params], histories=[state.history], rngs=[rng])
+    _, toks = engine(dev).sample_batch(logits, [params], histories=[state.history], rngs=[rng],
+                                       decoder=state.decoder)
     return int(toks[0])
 
 

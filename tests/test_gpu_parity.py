@@ -557,7 +557,7 @@ def test_device_decode_state(eng, V):
     seeds = [900 + b for b in range(B)]
     prompt = [rng.integers(0, V, size=int(rng.integers(0, 5))).astype(np.uint32) for _ in range(B)]
     cap = 64
-    ds = DeviceDecodeState(seeds, cap=cap, histories=prompt)
+    ds = DeviceDecodeState(eng, seeds, cap=cap, histories=prompt)
     host_rng = [Xorshift64(s) for s in seeds]
     hist = [list(p) for p in prompt]
     steps = 20 if V < 10000 else 6
@@ -599,7 +599,7 @@ def test_device_history_rewrite(eng):
               SP(temperature=0.0, presence_penalty=2.0, repeat_last_n=1),
               SP(temperature=1.0, top_k=30, repetition_penalty=1.3, repeat_last_n=5)]
     seeds = [1, 2, 3, 4]
-    ds = DeviceDecodeState(seeds, cap=32, histories=[[1, 2, 3]] * B)
+    ds = DeviceDecodeState(eng, seeds, cap=32, histories=[[1, 2, 3]] * B)
     hist = [[1, 2, 3] for _ in range(B)]
     host_rng = [Xorshift64(s) for s in seeds]
     for phase in range(2):
@@ -637,7 +637,7 @@ def test_device_history_overflow(eng):
               SP(temperature=0.0, repetition_penalty=1.5, repeat_last_n=8),
               SP(temperature=0.0)]
     hist = [list(range(20))] * 3
-    ds = DeviceDecodeState([1, 2, 3], cap=16, histories=hist)
+    ds = DeviceDecodeState(eng, [1, 2, 3], cap=16, histories=hist)
     lg = torch.from_numpy(np.random.default_rng(3).standard_normal((3, V)).astype(np.float32)).cuda()
     tr = torch.zeros((3, 16), dtype=torch.int32, device="cuda:0")
     toks, _ = ds.step(eng, lg, params, trace=tr, sync=False)
@@ -733,7 +733,7 @@ def test_decode_step_in_a_graph(eng):
            for _ in range(steps)]
     x = torch.empty((B, V), dtype=torch.float32, device="cuda:0")
     # eager
-    de = DeviceDecodeState(seeds, cap=256, histories=prompts)
+    de = DeviceDecodeState(eng, seeds, cap=256, histories=prompts)
     te = torch.empty(B, dtype=torch.int32, device="cuda:0")
     want = []
     for st in range(steps):
@@ -742,8 +742,8 @@ def test_decode_step_in_a_graph(eng):
         want.append(te.cpu().tolist())
     # warm-up on a throwaway state (the context allocates its buffers here),
     # then capture one step of a fresh state
-    dw = DeviceDecodeState(seeds, cap=256, histories=prompts)
-    dg = DeviceDecodeState(seeds, cap=256, histories=prompts)
+    dw = DeviceDecodeState(eng, seeds, cap=256, histories=prompts)
+    dg = DeviceDecodeState(eng, seeds, cap=256, histories=prompts)
     tg = torch.empty(B, dtype=torch.int32, device="cuda:0")
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
