@@ -460,7 +460,7 @@ def test_config3_full(eng):
 def test_config5_full(eng):
     from lumen_amd.workloads import config5
 
-    _run_workload(eng, config5(), n_rows=32)
+    _run_workload(eng, config5())
 
 
 def test_config4_full(eng):
@@ -482,10 +482,10 @@ def test_config2_sequential_draws(eng):
     rng = Xorshift64(w.seeds[0])
     hist = np.asarray(w.histories[0], dtype=np.uint32)
     lg = w.logits_f32()
-    for d in range(12):
+    for d in range(200):
         u = np.array([rng.next_f32()], np.float32)
         log(f"case config2 draw {d} history {hist.size}")
-        rep = parity.compare(eng, lg, w.params, [hist], u, check_pen=True)
+        rep = parity.compare(eng, lg, w.params, [hist], u, check_pen=d % 10 == 0)
         assert_clean(rep, f"config2 draw {d}")
         hist = np.append(hist, np.uint32(rep["gpu"][0]))
 
