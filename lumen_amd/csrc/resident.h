@@ -213,7 +213,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   double tot;
   const double P = p_slice + block_excl_scan_f64(d, s, &tot);
 #ifdef LUMEN_TIMING
-  LUMEN_TICK("rr_scan", 0);
+  LUMEN_TICK("rr_scan", LUMEN_TIMING_ROW);
 #endif
   const double rel = 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
   const uint32_t blo = est_binade(P * (1.0 - rel));
@@ -248,7 +248,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   const bool head = live && (unc || prv != code);
   const bool last = live && !unc && nxt != code;
 #ifdef LUMEN_TIMING
-  LUMEN_TICK("rr_maps", 0);
+  LUMEN_TICK("rr_maps", LUMEN_TIMING_ROW);
 #endif
   SegVal prev;
   const SegVal inc = seg_scan_incl(SegVal{head ? 1u : 0u, (live && !unc) ? own : PMap{0u, 0u}},
@@ -258,7 +258,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   const uint32_t pos = block_excl_scan_u32(packed, s, &ptot);
   RecCount rc{ptot & 0xffffu, ptot >> 16, true};
 #ifdef LUMEN_TIMING
-  LUMEN_TICK("rr_scans", 0);
+  LUMEN_TICK("rr_scans", LUMEN_TIMING_ROW);
 #endif
   if (rc.items > kResItemCap || rc.raws > kResRawCap) {
     rc.ok = false;
@@ -492,6 +492,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
       const float e3 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 3], m1));
       *reinterpret_cast<float4*>(Lt + 4 * q) = make_float4(e0, e1, e2, e3);
     }
+    LUMEN_TICK("rb_exps", b);
 #ifdef LUMEN_RES_STOP
     if (LUMEN_RES_STOP == 2) {
       if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
@@ -514,6 +515,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     }
     __syncthreads();
     for (uint32_t i = t; i < kBins; i += kThreads) hg[i] = hl[i];
+    LUMEN_TICK("rb_hist", b);
     const uint32_t nthr = (sc.hi - sc.lo + kResK - 1u) / kResK;
     const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, sl), s);
     if (t == 0) {
@@ -773,17 +775,27 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     atomicOr(&kbits[f >> 5], 1u << (f & 31u));
   }
   __syncthreads();
+  // at T = 1 without min-p the final softmax sums the kept values' own
+  // exp(v - m1): they travel in the list in place of the keys
+  const bool pre_exp = P.inv_temp == 1.0f && !(P.flags & kMinP);
   uint32_t nk;
   {
     const uint32_t kmask = (kbits[t >> 2] >> (8u * (t & 3u))) & 0xffu;  // candidates 8t .. 8t+7
+    const uint32_t* cande = reinterpret_cast<const uint32_t*>(cand + kCandCap);
     uint64_t cv[kPer];
+    uint32_t ev[kPer];
 #pragma unroll
-    for (int q = 0; q < (int)kPer; ++q) cv[q] = (kmask >> q) & 1u ? s.A[kPer * t + (uint32_t)q] : 0ull;
+    for (int q = 0; q < (int)kPer; ++q) {
+      const bool in = (kmask >> q) & 1u;
+      cv[q] = in ? s.A[kPer * t + (uint32_t)q] : 0ull;
+      ev[q] = in && pre_exp ? cande[kPer * t + (uint32_t)q] : 0u;
+    }
     uint32_t ko = block_excl_scan_u32((uint32_t)__popc(kmask), s, &nk);
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q)
       if ((kmask >> q) & 1u)
-        s.A[ko++] = ((uint64_t)(uint32_t)cv[q] << 32) | tkey(__uint_as_float((uint32_t)(cv[q] >> 32)));
+        s.A[ko++] = ((uint64_t)(uint32_t)cv[q] << 32) |
+                    (pre_exp ? ev[q] : tkey(__uint_as_float((uint32_t)(cv[q] >> 32))));
     __syncthreads();
   }
   RowTrace tr;
@@ -799,7 +811,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   LUMEN_TICK("r_kept", b);
   RES_STOP(9);
   // the nucleus holds the row maximum m1 (the largest p)
-  const uint32_t tok = final_on_list(a, P, nk, rdraw, s, tr, m1);
+  const uint32_t tok = final_on_list(a, P, nk, rdraw, s, tr, m1, pre_exp);
   LUMEN_TICK("r_final", b);
   write_result(a, b, tok, tr);
 }

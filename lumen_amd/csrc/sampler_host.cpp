@@ -68,7 +68,7 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
   // slice weights of the greedy, top-k and top-p paths; LUMEN_SAMPLER_WEIGHTS=g,k,p
   // overrides them (a tuning aid)
   struct Weights {
-    uint32_t g = 1, k = 2, p = 10;
+    uint32_t g = 2, k = 3, p = 8;
   };
   static const Weights wt = [] {
     Weights x;
@@ -90,11 +90,34 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
     wsum += w[b];
   }
   const uint32_t spare = cap > fixed ? cap - fixed : 0;
+  // fewest slices that keep a top-p row on the register-resident path
+  uint32_t g_res = 1;
+  while (g_res < lumen::kMaxSlices && ((V + g_res - 1u) / g_res + 15u) / 16u * 16u > kResSlice) ++g_res;
+  std::vector<uint8_t> res(B, 0);
+  uint64_t used = 0;
   for (uint32_t b = 0; b < B; ++b) {
     if (!w[b]) continue;
     uint64_t g = wsum ? ((uint64_t)spare * w[b] + wsum / 2) / wsum : 1;
     G[b] = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(g, lumen::kMaxSlices));
+    const RowParams& r = rows[b];
+    res[b] = (r.flags & lumen::kTopP) && !(r.flags & (lumen::kTopK | lumen::kGreedy)) ? 1 : 0;
+    if (res[b] && G[b] < g_res) G[b] = g_res;
     if (row_path(rows[b], V, G[b]) == kPathSingle) G[b] = 1;
+    used += G[b];
+  }
+  // raising top-p rows to g_res may overrun the spare workgroups: take them
+  // back from the rows with the most slices, keeping top-p rows at g_res
+  while (used > spare) {
+    uint32_t pick = B;
+    for (uint32_t b = 0; b < B; ++b) {
+      const uint32_t floor = res[b] ? g_res : 1u;
+      if (G[b] > floor && (pick == B || G[b] > G[pick])) pick = b;
+    }
+    if (pick == B) break;  // every row at its floor: the XCD packing below trims
+    uint32_t g = G[pick] - 1u;
+    if (row_path(rows[pick], V, g) == kPathSingle) g = 1;
+    used -= G[pick] - g;
+    G[pick] = g;
   }
   // every row at g_uniform: the kernel's arithmetic mapping places the same
   // grid without a map (one dependent load less per workgroup)

@@ -48,17 +48,22 @@
 // once when that row's result is written.
 #ifdef LUMEN_TIMING
 #include <cstdio>
-// one log per slice of row 0 in device memory; the workgroup's log index
-// (or -1) sits in LDS
+#ifndef LUMEN_TIMING_ROW
+#define LUMEN_TIMING_ROW 0
+#endif
+// one log per slice of the traced row in device memory; the workgroup's log
+// index (or -1) sits in LDS
 __device__ unsigned long long g_tick_t[16][64];
 __device__ const char* g_tick_l[16][64];
+__device__ int g_tick_n[16];
 __shared__ int g_tick_slot;
 __shared__ int g_nticks;
 #define LUMEN_TICK(label, b)                                                   \
   do {                                                                        \
-    if (threadIdx.x == 0 && (b) == 0 && g_tick_slot >= 0 && g_nticks < 64) {  \
+    if (threadIdx.x == 0 && (b) == LUMEN_TIMING_ROW && g_tick_slot >= 0 && g_nticks < 64) {  \
       g_tick_t[g_tick_slot][g_nticks] = wall_clock64();                       \
       g_tick_l[g_tick_slot][g_nticks++] = label;                              \
+      g_tick_n[g_tick_slot] = g_nticks;                                       \
     }                                                                         \
   } while (0)
 #define LUMEN_TICK_INIT() \
@@ -67,18 +72,28 @@ __shared__ int g_nticks;
   } while (0)
 #define LUMEN_TICK_SLOT(row, sl) \
   do {                           \
-    if (threadIdx.x == 0) g_tick_slot = ((row) == 0 && (sl) < 16) ? (int)(sl) : -1; \
+    if (threadIdx.x == 0) g_tick_slot = ((row) == LUMEN_TIMING_ROW && (sl) < 16) ? (int)(sl) : -1; \
   } while (0)
 #define LUMEN_TICK_RESET(b) \
   do {                      \
-    if (threadIdx.x == 0 && (b) == 0) g_nticks = 0; \
+    if (threadIdx.x == 0 && (b) == LUMEN_TIMING_ROW) g_nticks = 0; \
   } while (0)
+// times from the earliest first tick of any slice of the row
 #define LUMEN_TICK_DUMP(b)                                                       \
   do {                                                                          \
-    if (threadIdx.x == 0 && (b) == 0 && g_tick_slot >= 0)                       \
-      for (int i_ = 1; i_ < g_nticks; ++i_)                                     \
-        printf("tick[%d] %s +%f us\n", g_tick_slot, g_tick_l[g_tick_slot][i_],  \
-               (double)(g_tick_t[g_tick_slot][i_] - g_tick_t[g_tick_slot][i_ - 1]) / 100.0); \
+    if (threadIdx.x == 0 && (b) == LUMEN_TIMING_ROW && g_tick_slot >= 0) {      \
+      unsigned long long t0_ = ~0ull;                                           \
+      for (int k_ = 0; k_ < 16; ++k_)                                           \
+        if (g_tick_n[k_] > 0 && g_tick_t[k_][0] < t0_) t0_ = g_tick_t[k_][0];   \
+      for (int k_ = 0; k_ < 16; ++k_)                                           \
+        if (k_ != g_tick_slot && g_tick_n[k_] > 0)                              \
+          printf("tick[%d] last %s %f us\n", k_, g_tick_l[k_][g_tick_n[k_] - 1], \
+                 (double)(g_tick_t[k_][g_tick_n[k_] - 1] - t0_) / 100.0);       \
+      for (int i_ = 0; i_ < g_nticks; ++i_)                                     \
+        printf("tick[%d] %s %f us\n", g_tick_slot, g_tick_l[g_tick_slot][i_],  \
+               (double)(g_tick_t[g_tick_slot][i_] - t0_) / 100.0);              \
+      for (int k_ = 0; k_ < 16; ++k_) g_tick_n[k_] = 0;                         \
+    }                                                                           \
   } while (0)
 #else
 #define LUMEN_TICK(label, b) do { } while (0)
@@ -918,10 +933,30 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
 // n entries, every entry alive). Applies min-p, temperature, softmax, draw.
 // known_max: the largest logit of the list when the caller knows it (the
 // list is NaN-free then), NaN otherwise.
+// With pre_exp, list entries carry exp(v - known_max) in place of the key:
+// the caller computed them exactly (expf_glibc) and guarantees inv_temp == 1,
+// no min-p, and a finite known_max equal to the list maximum, so the
+// summands of the final softmax are those values themselves.
 __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const RowParams P, uint32_t n, float r,
-                                  Smem& s, RowTrace& tr, float known_max) {
+                                  Smem& s, RowTrace& tr, float known_max, bool pre_exp = false) {
   const uint32_t V = a.vocab;
   auto lv = [&](uint32_t j) -> float { return key2f((uint32_t)s.A[j]); };
+  if (pre_exp) {
+    float* xs = reinterpret_cast<float*>(s.Bk);
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __uint_as_float((uint32_t)s.A[j]);
+    __syncthreads();
+    tr.final_max = known_max;
+    const EcssResult S = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssSum, 0.f, 0.f, s);
+    const float S3 = S.c;
+    for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
+    __syncthreads();
+    tr.final_sum = S3;
+    const EcssResult e = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
+    tr.cdf_before = e.found ? e.before : e.c;
+    tr.cdf_at = e.c;
+    if (e.found) return (uint32_t)(s.A[e.pos] >> 32);
+    return V - 1;
+  }
 #ifdef LUMEN_TICK_FINAL
   LUMEN_TICK_RESET(0);
   LUMEN_TICK("final_start", 0);
@@ -963,7 +998,7 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
     m3 = block_rmax(m3, s);
     nan3 = block_or_u32(nan3, s);
   }
-  LUMEN_TICK("fin_m3", 0);
+  LUMEN_TICK("fin_m3", LUMEN_TIMING_ROW);
   tr.final_max = m3;
   if (!is_finite(m3)) {
     tr.path |= 16u;
@@ -987,6 +1022,7 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
   float* xs = reinterpret_cast<float*>(s.Bk);
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = expf_glibc(__fsub_rn(wv(j), m3));
   __syncthreads();
+  LUMEN_TICK("fin_exps", LUMEN_TIMING_ROW);
 #ifdef LUMEN_RES_STOP
   if (LUMEN_RES_STOP == 20) return 0;
 #endif
@@ -997,14 +1033,14 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
 #endif
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
   __syncthreads();
-  LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", 0);
+  LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", LUMEN_TIMING_ROW);
   tr.final_sum = S3;
   EcssResult e = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
 #ifdef LUMEN_RES_STOP
   if (LUMEN_RES_STOP == 22) return 0;
 #endif
-  LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", 0);
-  LUMEN_TICK("fin_walk", 0);
+  LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", LUMEN_TIMING_ROW);
+  LUMEN_TICK("fin_walk", LUMEN_TIMING_ROW);
   tr.cdf_before = e.found ? e.before : e.c;
   tr.cdf_at = e.c;
   if (e.found) return (uint32_t)(s.A[e.pos] >> 32);
