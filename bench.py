@@ -91,10 +91,14 @@ def cpu_baseline(w, uniforms, budget_s=20.0):
     rows = 0
     t0 = time.perf_counter()
     reps = 0
-    while True:
+    done = False
+    while not done:
         for b in range(w.batch):
             o.sample_logits_r(lg[b], ops[b], w.histories[b], float(uniforms[b]))
             rows += 1
+            if time.perf_counter() - t0 > budget_s:
+                done = True
+                break
         reps += 1
         el = time.perf_counter() - t0
         if el > budget_s / 2 or reps >= 5:
@@ -243,17 +247,220 @@ def b1_graph_decode(eng, per_graph=32, replays=20):
     return dt / (replays * per_graph) * 1e6, replays * per_graph
 
 
+def oracle_params(w):
+    from oracle import oracle as o
+
+    return [o.Params(temperature=p.temperature, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p,
+                     repetition_penalty=p.repetition_penalty, presence_penalty=p.presence_penalty,
+                     frequency_penalty=p.frequency_penalty, repeat_last_n=p.repeat_last_n)
+            for p in w.params]
+
+
+def row_kind(p):
+    if p.temperature <= 0:
+        return "greedy"
+    return "+".join(k for k, on in (("top_k", p.top_k), ("top_p", p.top_p), ("min_p", p.min_p),
+                                      ("penalties", p.penalties_active())) if on) or "plain"
+
+
+def logit_variants(name, w, total_bytes):
+    """The workload's logits plus further draws of the same generator (other
+    seeds), enough buffers that cycling through them exceeds `total_bytes`
+    (the MI355X's 256 MB Infinity Cache), so every launch reads HBM."""
+    from lumen_amd import workloads
+
+    per = w.logits.nbytes
+    k = max(1, min(8, -(-total_bytes // per)))
+    gen = workloads.CONFIGS[name]
+    out = [w.logits]
+    for j in range(1, k):
+        out.append(gen(seed=1000 + 17 * j).logits)
+    return out
+
+
+def to_device(w, lg):
+    import torch
+
+    if w.dtype == "bf16":
+        return torch.from_numpy(np.ascontiguousarray(lg).view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(lg)).cuda()
+
+
+def parity_check(w, lgs, toks, traces, u_host, threads):
+    """Tokens of the timed buffers against the oracle (outside the timed
+    region). A mismatch counts as inside the 1e-6 zone when the draw lies
+    within 1e-6 of the CDF value at or before the token (GPU trace)."""
+    from oracle import oracle as o
+
+    ops = oracle_params(w)
+    out = {"rows": 0, "match": 0, "mismatch_in_1e-6": 0, "mismatch_outside": 0,
+           "greedy_rows": 0, "greedy_exact": 0, "topk_rows": 0, "topk_set_exact": 0}
+    for lg, tk, tr in zip(lgs, toks, traces):
+        lf = lg if w.dtype == "f32" else (lg.astype(np.uint32) << 16).view(np.float32)
+        ref = o.sample_batch(lf, ops, w.histories, u_host, threads=threads)
+        for b in range(w.batch):
+            out["rows"] += 1
+            ok = int(ref[b]) == int(tk[b])
+            if w.params[b].temperature <= 0:
+                out["greedy_rows"] += 1
+                out["greedy_exact"] += int(ok)
+            if ok:
+                out["match"] += 1
+                continue
+            cb, ca = tr[b, 10].view(np.float32), tr[b, 11].view(np.float32)
+            near = min(abs(float(u_host[b]) - float(ca)), abs(float(u_host[b]) - float(cb))) <= 1e-6
+            out["mismatch_in_1e-6" if near else "mismatch_outside"] += 1
+    # top-k candidate sets (cutoff key and survivor count) on the first buffer
+    lf = lgs[0] if w.dtype == "f32" else (lgs[0].astype(np.uint32) << 16).view(np.float32)
+    for b, p in enumerate(w.params):
+        if p.temperature > 0 and p.top_k and p.top_k < w.vocab:
+            _, rt = o.sample_logits_r(lf[b], ops[b], w.histories[b], float(u_host[b]))
+            out["topk_rows"] += 1
+            tr = traces[0][b]
+            out["topk_set_exact"] += int(rt["topk_survivors"] == int(tr[3]) and
+                                         rt["topk_cutoff_key"] == int(tr[2]))
+    return out
+
+
+def measure(eng, name, steps, warmup, graph, rotate_bytes, cpu=True, cpu_budget=12.0):
+    """One workload: `steps` timed launches (HIP graph replays of `graph`
+    launches, cycling through the rotated logits buffers), kernel time from
+    HIP events on the launch stream, parity of the timed tokens, and the CPU
+    oracle on the same rows."""
+    import torch
+
+    from lumen_amd import workloads
+
+    w = workloads.CONFIGS[name]()
+    B, V = w.logits.shape
+    lgs = logit_variants(name, w, rotate_bytes)
+    devs = [to_device(w, lg) for lg in lgs]
+    nbuf = len(devs)
+    csr = penalty_csr(w, devs[0].device)
+    u_host = first_draws(w)
+    u_dev = torch.from_numpy(u_host).cuda()
+    toks = [torch.empty(B, dtype=torch.int32, device="cuda") for _ in range(nbuf)]
+    pbs = [eng.prepare(d, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=t)
+           for d, t in zip(devs, toks)]
+    for i in range(warmup):
+        pbs[i % nbuf].run(sync=False)
+    torch.cuda.synchronize()
+    # stream launches, one HIP-event pair per step
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        pbs[i % nbuf].run(sync=False)
+        ends[i].record()
+    torch.cuda.synchronize()
+    el_stream = time.perf_counter() - t0
+    kern_stream = float(np.mean([a.elapsed_time(b) for a, b in zip(starts, ends)]))
+    el, kern_ms, mode = el_stream, kern_stream, "stream launches"
+    if graph > 1 and steps >= graph:
+        # the launch-bound loop captured, as a serving loop captures its
+        # sampler: each launch is one kernel node (parameters and draws are
+        # resident), every replay runs the full kernel over its buffer
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            gpbs = [eng.prepare(d, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=t)
+                    for d, t in zip(devs, toks)]
+            for i in range(graph):
+                gpbs[i % nbuf].run(sync=False)
+        g.replay()
+        torch.cuda.synchronize()
+        reps, rem = divmod(steps, graph)
+        gs = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+        ge = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(reps):
+            gs[i].record()
+            g.replay()
+            ge[i].record()
+        for i in range(rem):
+            pbs[i % nbuf].run(sync=False)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        kern_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(gs, ge)])) / graph
+        mode = f"HIP graph replays of {graph} launches"
+    logit_bytes = B * V * (2 if w.dtype == "bf16" else 4)
+    achieved = logit_bytes / (kern_ms * 1e-3) / 1e9
+    # traces of one more call per buffer: passes and CDF values for parity
+    traces = []
+    for d, t in zip(devs, toks):
+        tr = torch.zeros((B, 16), dtype=torch.int32, device="cuda")
+        eng.sample_batch(d, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=t,
+                         trace=tr, sync=False)
+        traces.append(tr)
+    torch.cuda.synchronize()
+    traces = [tr.cpu().numpy().view(np.uint32) for tr in traces]
+    tok_host = [t.cpu().numpy().view(np.uint32) for t in toks]
+    kinds = {}
+    for b, p in enumerate(w.params):
+        kinds.setdefault(row_kind(p), []).append(int(traces[0][b, 13]))
+    res = {
+        "workload": workload_desc(w),
+        "batch": B, "vocab": V, "dtype": "f32" if w.dtype == "f32" else "bf16",
+        "samples_per_s": round(B * steps / el, 1),
+        "us_per_sample": round(el / steps / B * 1e6, 4),
+        "ms_per_step": round(el / steps * 1e3, 4),
+        "launch": mode,
+        "stream_launches": {"samples_per_s": round(B * steps / el_stream, 1),
+                            "kernel_ms": round(kern_stream, 5)},
+        "logit_buffers": {"count": nbuf, "bytes": int(sum(lg.nbytes for lg in lgs)),
+                          "why": "cycled so that every launch reads its logits from HBM, "
+                                 "not from the 256 MB Infinity Cache"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles(f"lumen_sample_rows_{name}_pmc.txt"),
+                     "kernel": "lumen_sample_rows", "kernel_ms": round(kern_ms, 5),
+                     "bytes_per_launch": logit_bytes},
+        "logit_passes_per_row": {k: round(float(np.mean(v)), 2) for k, v in kinds.items()},
+    }
+    nt = host_cores()
+    res["parity"] = parity_check(w, lgs, tok_host, traces, u_host, nt)
+    if cpu:
+        rate, rows, reps, cel = cpu_baseline(w, u_host, budget_s=cpu_budget)
+        res["cpu_baseline"] = {"value": round(rate, 2), "unit": "samples/s", "cores": 1,
+                               "kind": "port",
+                               "sample": f"{w.name}: {rows} rows ({reps} passes over the first "
+                                         f"buffer, {cel:.1f} s), same inputs, single thread, "
+                                         "oracle/sampling_ref.c -O2",
+                               "cpu": cpu_model()}
+        if nt > 1:
+            rate_mt, rows_mt, reps_mt, cel_mt = cpu_baseline_threads(w, u_host, nt,
+                                                                     budget_s=cpu_budget / 2)
+            res["cpu_baseline_all_cores"] = {
+                "value": round(rate_mt, 2), "unit": "samples/s", "cores": nt, "kind": "port",
+                "sample": f"{w.name}: {rows_mt} rows ({reps_mt} passes, {cel_mt:.1f} s), rows "
+                          f"split over {nt} threads"}
+    return res
+
+
+def workload_desc(w):
+    kinds = {}
+    for p in w.params:
+        kinds[row_kind(p)] = kinds.get(row_kind(p), 0) + 1
+    mix = ", ".join(f"{n} {k}" for k, n in kinds.items())
+    return f"{w.name}: B={w.batch} V={w.vocab} {w.dtype} logits; rows: {mix}"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="config3")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-b1", action="store_true", help="skip the B=1 latency leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-b1", action="store_true", help="skip the B=1 latency legs")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="measure only the headline workload (no per-config entries)")
     ap.add_argument("--b1-draws", type=int, default=10_000)
     ap.add_argument("--graph", type=int, default=10,
-                    help="also time the steps as replays of a HIP graph of this many launches")
+                    help="time the steps as replays of a HIP graph of this many launches")
+    ap.add_argument("--rotate-mb", type=int, default=300,
+                    help="cycle through logits buffers totalling at least this many MB")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB device copy (PMC calibration)")
     args = ap.parse_args()
@@ -276,115 +483,37 @@ def main():
         print(json.dumps({"copy_bytes_read": a.numel() * 4, "copy_bytes_written": b.numel() * 4}))
         return
 
-    from lumen_amd import workloads
     from lumen_amd.sampling import Engine
 
-    w = workloads.CONFIGS[args.workload]()
-    B, V = w.logits.shape
     eng = Engine(0)
-    if w.dtype == "bf16":
-        dev = torch.from_numpy(w.logits.view(np.int16)).view(torch.bfloat16).cuda()
-    else:
-        dev = torch.from_numpy(w.logits).cuda()
-    csr = penalty_csr(w, dev.device)
-    u_host = first_draws(w)
-    u_dev = torch.from_numpy(u_host).cuda()
-    tok = torch.empty(B, dtype=torch.int32, device=dev.device)
-
-    def step():
-        eng.sample_batch(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=tok,
-                         sync=False)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    # stream launches, one HIP-event pair per step
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record()
-        step()
-        ends[i].record()
-    torch.cuda.synchronize()
-    el_stream = time.perf_counter() - t0
-    kern_ms_stream = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
-    el, kern_ms, mode = el_stream, kern_ms_stream, "stream launches"
-    if args.graph > 1:
-        # The same K steps as replays of a HIP graph of `graph` sampler
-        # launches (parameters and draws are resident, so each launch records
-        # one kernel node and nothing else): the launch-bound loop captured,
-        # as a serving loop that captures its sampler runs it. Any remainder
-        # of K runs as stream launches inside the timed region.
-        pb = eng.prepare(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=tok)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            gpb = eng.prepare(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev,
-                              tokens_out=tok)
-            for _ in range(args.graph):
-                gpb.run(sync=False)
-        g.replay()
-        torch.cuda.synchronize()
-        reps, rem = divmod(args.steps, args.graph)
-        gs = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-        ge = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(reps):
-            gs[i].record()
-            g.replay()
-            ge[i].record()
-        for _ in range(rem):
-            pb.run(sync=False)
-        torch.cuda.synchronize()
-        el = time.perf_counter() - t0
-        if reps:
-            kern_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(gs, ge)])) / args.graph
-        mode = f"HIP graph replays of {args.graph} launches"
-
-    logit_bytes = B * V * (2 if w.dtype == "bf16" else 4)
-    achieved = logit_bytes / (kern_ms * 1e-3) / 1e9
-    value = B * args.steps / el
+    rot = args.rotate_mb * 2**20
+    head = measure(eng, args.workload, args.steps, args.warmup, args.graph, rot,
+                   cpu=not args.no_cpu, cpu_budget=20.0)
     line = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": head["samples_per_s"],
         "unit": "samples/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(el / args.steps * 1e3, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if w.dtype == "f32" else "bf16",
+        "dtype": head["dtype"],
         "data": "synthetic (seeded generators in lumen_amd/workloads.py)",
-        "config": {"workload": f"{w.name}: B={B} V={V} {w.dtype} logits, mixed sampling rows",
-                   "batch": B, "vocab": V},
-        "us_per_sample": round(el / args.steps / B * 1e6, 4),
-        "launch": mode,
-        "stream_launches": {"value": round(B * args.steps / el_stream, 1),
-                            "ms_per_step": round(el_stream / args.steps * 1e3, 4),
-                            "kernel_ms": round(kern_ms_stream, 5)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles(f"lumen_sample_rows_{w.name}_pmc.txt"),
-                     "kernel": "lumen_sample_rows", "kernel_ms": round(kern_ms, 5),
-                     "bytes_per_launch": logit_bytes},
+        "config": {"workload": head["workload"], "batch": head["batch"], "vocab": head["vocab"]},
+        "us_per_sample": head["us_per_sample"],
+        "launch": head["launch"],
+        "stream_launches": head["stream_launches"],
+        "logit_buffers": head["logit_buffers"],
+        "roofline": head["roofline"],
+        "logit_passes_per_row": head["logit_passes_per_row"],
+        "parity": head["parity"],
     }
-    # logit passes per row, from the row traces of one more call
-    trace = torch.zeros((B, 16), dtype=torch.int32, device=dev.device)
-    eng.sample_batch(dev, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=tok,
-                     trace=trace, sync=False)
-    torch.cuda.synchronize()
-    passes = trace.cpu().numpy().view(np.uint32)[:, 13]
-    kinds = {}
-    for b, p in enumerate(w.params):
-        kind = ("greedy" if p.temperature <= 0 else
-                "+".join(k for k, on in (("top_k", p.top_k), ("top_p", p.top_p),
-                                          ("penalties", p.penalties_active())) if on) or "plain")
-        kinds.setdefault(kind, []).append(int(passes[b]))
-    line["logit_passes_per_row"] = {k: round(float(np.mean(v)), 2) for k, v in kinds.items()}
+    for k in ("cpu_baseline", "cpu_baseline_all_cores"):
+        if k in head:
+            line[k] = head[k]
     if not args.no_b1:
         p50, p99, n, api50 = b1_latency(eng, args.b1_draws)
         line["b1_latency"] = {"p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
@@ -403,21 +532,15 @@ def main():
             "p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
             "workload": "config2 decode loop: RNG state and a 8192-token history ring on "
                         "the device, whole-history penalty window counted per draw"}
-    if not args.no_cpu:
-        rate, rows, reps, cel = cpu_baseline(w, u_host)
-        line["cpu_baseline"] = {"value": round(rate, 2), "unit": "samples/s", "cores": 1,
-                                "kind": "port",
-                                "sample": f"{w.name}: all {B} rows x {reps} passes "
-                                          f"({rows} samples, {cel:.1f} s), same inputs, "
-                                          "single thread, oracle/sampling_ref.c -O2",
-                                "cpu": cpu_model()}
-        nt = host_cores()
-        if nt > 1:
-            rate_mt, rows_mt, reps_mt, cel_mt = cpu_baseline_threads(w, u_host, nt)
-            line["cpu_baseline_all_cores"] = {
-                "value": round(rate_mt, 2), "unit": "samples/s", "cores": nt, "kind": "port",
-                "sample": f"{w.name}: all {B} rows x {reps_mt} passes ({rows_mt} samples, "
-                          f"{cel_mt:.1f} s), rows split over {nt} threads"}
+    if not args.no_configs:
+        line["configs"] = {}
+        for name, steps in (("config1", 200), ("config4", 40), ("config5", 100),
+                            ("defaults", 40)):
+            if name == args.workload:
+                continue
+            print(f"bench: measuring {name}", file=sys.stderr, flush=True)
+            line["configs"][name] = measure(eng, name, steps, 5, 10, rot, cpu=not args.no_cpu,
+                                            cpu_budget=8.0)
     eng.close()
     print(json.dumps(line))
 

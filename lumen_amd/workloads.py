@@ -136,5 +136,34 @@ def config5(seed=5, V=248_320, B=128) -> Workload:
     return Workload("config5", lg, "f32", params, hists, [seed * 1000 + b for b in range(B)])
 
 
+def defaults(seed=6, V=248_320, B=64) -> Workload:
+    """The parameter sets real callers send most, on config 3's logits
+    distribution: 16 rows of the reference default SamplingParams (T 1.0,
+    nothing else; sampling.rs:313-325), 16 of the server default for a
+    request without top_p (T 0.7, repetition penalty 1.05;
+    runtime_defaults.rs:431, :486), 16 of that with top_p 0.9, and 16 with
+    min_p 0.05 + top_p 0.95 + top_k 4,096 (T 0.8)."""
+    rng = np.random.default_rng(seed)
+    lg = rng.normal(0.0, 3.0, size=(B, V)).astype(np.float32)
+    lg += rng.gumbel(0.0, 1.0, size=(B, V)).astype(np.float32)
+    perm = rng.permutation(V)
+    params, hists = [], []
+    q = max(B // 4, 1)
+    for b in range(B):
+        kind = min(b // q, 3)
+        if kind == 0:
+            p = SamplingParams(temperature=1.0)
+        elif kind == 1:
+            p = SamplingParams(temperature=0.7, repetition_penalty=1.05)
+        elif kind == 2:
+            p = SamplingParams(temperature=0.7, repetition_penalty=1.05, top_p=0.9)
+        else:
+            p = SamplingParams(temperature=0.8, top_k=4096, top_p=0.95, min_p=0.05)
+        params.append(p)
+        hists.append(zipf_ids(rng, int(rng.integers(0, 4097)), V, 1.1, perm))
+    return Workload("defaults", lg, "f32", params, hists, [seed * 1000 + b for b in range(B)])
+
+
 CONFIGS = {"config1": config1, "config1_greedy": config1_greedy, "config2": config2,
-           "config3": config3, "config4": config4, "config5": config5}
+           "config3": config3, "config4": config4, "config5": config5,
+           "defaults": defaults}
