@@ -71,6 +71,10 @@ constexpr int kCandCap = 8192;      // per-row candidate buffer (entries)
 // Row stride of the candidate buffers: kCandCap entries, then (register-
 // resident top-p rows) each candidate's exp(v - m1) as a u32 array.
 constexpr int kCandStride = 2 * kCandCap;
+// Split top-k rows take k up to kTopKSplitMax; their candidates may fill the
+// whole row stride of the candidate buffer.
+constexpr uint32_t kTopKSplitMax = 4096;
+constexpr uint32_t kTopKCandCap = (uint32_t)kCandStride;
 constexpr int kMassBins = 512;      // top-p window planning bins
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
 constexpr int kRowRecs = kMaxSlices * kChainMaxQ * 16;  // run records per row (one per wave segment)

@@ -196,8 +196,14 @@ struct RecCount {
 //                          when the exact sum is inside bin at its start and
 //                          stays there), else its 32 summands at raw slot r.
 // Items start at rec[0]; raw slot r at rec[kResRawOff + 32 r].
+// FIND (inverse-CDF records): a thread whose running-sum range may hold the
+// draw `probe` is made uncertain too, so a search for the first sum above
+// the probe always ends inside a raw; raw items carry their thread index in
+// bits 16..25 of the last word.
+template <bool FIND = false>
 __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, uint32_t pos0,
-                                               uint32_t nthr, uint32_t* rec, Smem& s) {
+                                               uint32_t nthr, uint32_t* rec, Smem& s,
+                                               float probe = 0.f) {
   const uint32_t t = threadIdx.x;
   const bool live = t < nthr;
   const float4* e4 = reinterpret_cast<const float4*>(et);  // this thread's 32 summands (LDS)
@@ -218,7 +224,8 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   const double rel = 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
   const uint32_t blo = est_binade(P * (1.0 - rel));
   const uint32_t bhi = est_binade((P + d) * (1.0 + rel));
-  const bool unc = live && blo != bhi;
+  bool unc = live && blo != bhi;
+  if (FIND) unc = unc || (live && P * (1.0 - rel) <= (double)probe && (double)probe <= (P + d) * (1.0 + rel));
   const uint32_t bin = unc ? est_binade(P + 0.5 * d) : blo;
   float y0 = __uint_as_float(bin), y1 = __uint_as_float(bin | 1u);
 #pragma unroll
@@ -266,7 +273,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   }
   const uint32_t ip = pos & 0xffffu, rp = pos >> 16;
   if (unc) {
-    *reinterpret_cast<uint4*>(rec + 4u * ip) = make_uint4(bin, own.a0, own.a1, rp);
+    *reinterpret_cast<uint4*>(rec + 4u * ip) = make_uint4(bin, own.a0, own.a1, FIND ? rp | (t << 16) : rp);
     uint4* raw = reinterpret_cast<uint4*>(rec + kResRawOff + kResK * rp);
     const uint4* u4 = reinterpret_cast<const uint4*>(et);
 #pragma unroll
@@ -326,13 +333,51 @@ __device__ __forceinline__ uint32_t res_sample_select(const float (&smp)[4], uin
   return tau;
 }
 
-// Top-p (no top-k) over a register-resident slice; see the header comment.
+// Loads virtual slice sc into x (thread t: elements 32t .. 32t+31) with the
+// penalties applied (sampling.rs:881-900, each history id once). The loads
+// v must have been issued for sc (res_issue).
 template <bool BF16>
+__device__ __forceinline__ void res_load(const KernelArgs& a, int b, const RowParams& P,
+                                         const Row& row, Slice sc, bool pen,
+                                         const float (&v)[8][4], float (&x)[kResK], Smem& s) {
+  const uint32_t t = threadIdx.x;
+  const bool tail = res_has_tail(row, sc);
+  res_transpose(v, x, s, pen || tail, [&](float* L) {
+    if (tail) {
+      res_tail(row, sc, L);
+      if (pen) __syncthreads();
+    }
+    if (!pen) return;
+    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
+    for (uint32_t j = h0 + t; j < h1; j += kThreads) {
+      const uint32_t id = a.hist_ids[j];
+      if (id >= sc.lo && id < sc.hi) {
+        float& y = L[res_slot(id - sc.lo)];
+        y = penalize(y, a.hist_cnt[j], P);
+      }
+    }
+  });
+}
+
+// Chunks per workgroup of a register-resident row with G workgroups: the
+// fewest q (at most 4, G * q <= kMaxSlices) whose G * q virtual slices each
+// fit kResSlice logits; 0 when none does.
+__device__ __forceinline__ uint32_t res_chunks(uint32_t V, uint32_t G) {
+  for (uint32_t q = 1; q <= 4u && G * q <= (uint32_t)kMaxSlices; ++q)
+    if ((((V + G * q - 1u) / (G * q) + 15u) & ~15u) <= kResSlice) return q;
+  return 0u;
+}
+
+// Top-p (no top-k) over register-resident slices; see the header comment.
+// Workgroup sl owns the q virtual slices sl*q .. sl*q+q-1 of the row's G*q;
+// with q > 1 each is read again (from cache) in phase B.
+template <bool BF16, bool MULTI>
 __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl, uint32_t G,
-                                         Smem& s) {
+                                         uint32_t q_rt, Smem& s) {
   ROW_CONTEXT(a, b);
+  const uint32_t q = MULTI ? q_rt : 1u;  // one chunk: straight-line code
   const uint32_t V = a.vocab, t = threadIdx.x, lane = t & 63u;
-  const Slice sc = slice_bounds(V, G, sl);
+  const uint32_t Gv = G * q;
   const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
   LUMEN_TICK("r_start", b);
 
@@ -346,7 +391,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   float smp[4];
   res_sample_issue(row, smp);
   float v[8][4];
-  res_issue<BF16>(row, sc, v);
+  res_issue<BF16>(row, slice_bounds(V, Gv, sl * q), v);
   const uint32_t tau = res_sample_select(smp, V, kResCandTarget, s);
   const float tv = tau ? key2f(tau) : kNegInf;
 #ifdef LUMEN_RES_STOP
@@ -359,59 +404,49 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   }
 #endif
   float x[kResK];
-  const bool tail = res_has_tail(row, sc);
-  res_transpose(v, x, s, pen || tail, [&](float* L) {
-    if (tail) {
-      res_tail(row, sc, L);
-      if (pen) __syncthreads();
-    }
-    if (!pen) return;
-    // sampling.rs:881-900 on the slice's history ids (each id once)
-    const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
-    for (uint32_t j = h0 + t; j < h1; j += kThreads) {
-      const uint32_t id = a.hist_ids[j];
-      if (id >= sc.lo && id < sc.hi) {
-        float& y = L[res_slot(id - sc.lo)];
-        y = penalize(y, a.hist_cnt[j], P);
-      }
-    }
-  });
-  LUMEN_TICK("r_loaded", b);
+  uint32_t cmask = 0, coff = 0;
+  for (uint32_t j = 0; j < q; ++j) {
+    const uint32_t vs = sl * q + j;
+    const Slice sc = slice_bounds(V, Gv, vs);
+    if (j > 0) res_issue<BF16>(row, sc, v);
+    res_load<BF16>(a, b, P, row, sc, pen, v, x, s);
+    LUMEN_TICK("r_loaded", b);
 #ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 12) {
-    float acc = 0.f;
-    for (int q = 0; q < (int)kResK; ++q) acc += x[q];
-    if (acc == 1234.5f) a.tokens[b] = 7u;
-    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-    return;
-  }
+    if (LUMEN_RES_STOP == 12) {
+      float acc = 0.f;
+      for (int q = 0; q < (int)kResK; ++q) acc += x[q];
+      if (acc == 1234.5f) a.tokens[b] = 7u;
+      if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
+      return;
+    }
 #endif
-  if (a.pen_out) {
-    float* po = a.pen_out + (uint64_t)b * V + sc.lo + t * kResK;
+    if (a.pen_out) {
+      float* po = a.pen_out + (uint64_t)b * V + sc.lo + t * kResK;
 #pragma unroll
-    for (int k = 0; k < (int)kResK; ++k)
-      if (sc.lo + t * kResK + (uint32_t)k < sc.hi) po[k] = x[k];
-  }
-  float mt = kNegInf;
-  uint32_t cmask = 0;
+      for (int k = 0; k < (int)kResK; ++k)
+        if (sc.lo + t * kResK + (uint32_t)k < sc.hi) po[k] = x[k];
+    }
+    float mt = kNegInf;
+    cmask = 0;
 #pragma unroll
-  for (int k = 0; k < (int)kResK; ++k) {
-    mt = op_maxl(mt, x[k]);
-    cmask |= (x[k] >= tv ? 1u : 0u) << k;  // NaN never qualifies
-  }
-  uint32_t ctot;
-  uint32_t coff = block_excl_scan_u32((uint32_t)__popc(cmask), s, &ctot);
-  const float ms = block_maxl(mt, s);
-  float et = 0.f;  // NaN in the slice makes the estimate NaN
-  if (ms != kNegInf) {
+    for (int k = 0; k < (int)kResK; ++k) {
+      mt = op_maxl(mt, x[k]);
+      cmask |= (x[k] >= tv ? 1u : 0u) << k;  // NaN never qualifies
+    }
+    uint32_t ctot;
+    coff = block_excl_scan_u32((uint32_t)__popc(cmask), s, &ctot);
+    const float ms = block_maxl(mt, s);
+    float et = 0.f;  // NaN in the slice makes the estimate NaN
+    if (ms != kNegInf) {
 #pragma unroll
-    for (int k = 0; k < (int)kResK; ++k) et += __expf(x[k] - ms);
-  }
-  const double es = block_sum_f64((double)et, s);
-  if (t == 0) {
-    ws.part_max[sl] = ms;
-    ws.part_e[sl] = es;
-    ws.part_cn[sl] = ctot;
+      for (int k = 0; k < (int)kResK; ++k) et += __expf(x[k] - ms);
+    }
+    const double es = block_sum_f64((double)et, s);
+    if (t == 0) {
+      ws.part_max[vs] = ms;
+      ws.part_e[vs] = es;
+      ws.part_cn[vs] = ctot;
+    }
   }
   LUMEN_TICK("r_phaseA", b);
 #ifdef LUMEN_RES_STOP
@@ -432,37 +467,53 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
 #endif
 
   // ---- phase B ----
-  // the row's values, one slice per lane of wave 0, in one round trip
-  float* rowv = reinterpret_cast<float*>(s.H0 + 1024);  // [0] m1, [2..3] p_slice (f64)
-  uint32_t* rowu = s.H0 + 1032;                        // [0] ncand, [1] bad, [2] candidate base
-  if (t < 64u) {
-    const bool in = lane < G;
-    const float mi = in ? ws.part_max[lane] : kNegInf;
-    const double ei = in ? ws.part_e[lane] : 0.0;
-    const uint32_t ci = in ? ws.part_cn[lane] : 0u;
-    const float m1w = wave_reduce(mi, kNegInf, op_maxl);
-    const double term = (lane < sl && mi != kNegInf) ? ei * exp((double)mi - (double)m1w) : 0.0;
-    const double ps = wave_reduce(term, 0.0, [](double l, double r) { return l + r; });
-    const uint32_t cin = wave_scan_incl(ci, 0u, op_add_u32);
-    const uint32_t nc = wave_read(cin, 63);
-    const bool nan = __ballot(in && !(ei == ei)) != 0ull;
-    if (lane == sl) rowu[2] = cin - ci;
-    if (lane == 0) {
-      rowv[0] = m1w;
-      *reinterpret_cast<double*>(rowv + 2) = ps;
-      rowu[0] = nc;
-      rowu[1] = (nan || !is_finite(m1w) || nc > (uint32_t)kCandCap) ? 1u : 0u;
-    }
-  }
-  __syncthreads();
-  const float m1 = rowv[0];
-  const double p_slice = *reinterpret_cast<const double*>(rowv + 2);
-  const uint32_t ncand = rowu[0];
-  const uint32_t cbase = rowu[2];
-  bool bad = !ok || rowu[1] != 0u;
-  float* hg = a.hist + ((uint64_t)b * kMaxSlices + sl) * kMassBins;
+  // the last chunk first: its logits are still in registers
   constexpr uint32_t kBins = (uint32_t)kMassBins;
-  if (!bad) {
+  bool bad = false;
+  float m1 = 0.f;
+  for (uint32_t jj = 0; jj < q; ++jj) {
+    const uint32_t j = q - 1u - jj;
+    const uint32_t vs = sl * q + j;
+    const Slice sc = slice_bounds(V, Gv, vs);
+    if (jj > 0) {
+      res_issue<BF16>(row, sc, v);
+      res_load<BF16>(a, b, P, row, sc, pen, v, x, s);
+      cmask = 0;
+#pragma unroll
+      for (int k = 0; k < (int)kResK; ++k) cmask |= (x[k] >= tv ? 1u : 0u) << k;
+      uint32_t ctot;
+      coff = block_excl_scan_u32((uint32_t)__popc(cmask), s, &ctot);
+    }
+    // the row's values, one virtual slice per lane of wave 0, in one round trip
+    float* rowv = reinterpret_cast<float*>(s.H0 + 1024);  // [0] m1, [2..3] p_slice (f64)
+    uint32_t* rowu = s.H0 + 1032;                        // [0] ncand, [1] bad, [2] candidate base
+    if (t < 64u) {
+      const bool in = lane < Gv;
+      const float mi = in ? ws.part_max[lane] : kNegInf;
+      const double ei = in ? ws.part_e[lane] : 0.0;
+      const uint32_t ci = in ? ws.part_cn[lane] : 0u;
+      const float m1w = wave_reduce(mi, kNegInf, op_maxl);
+      const double term = (lane < vs && mi != kNegInf) ? ei * exp((double)mi - (double)m1w) : 0.0;
+      const double ps = wave_reduce(term, 0.0, [](double l, double r) { return l + r; });
+      const uint32_t cin = wave_scan_incl(ci, 0u, op_add_u32);
+      const uint32_t nc = wave_read(cin, 63);
+      const bool nan = __ballot(in && !(ei == ei)) != 0ull;
+      if (lane == vs) rowu[2] = cin - ci;
+      if (lane == 0) {
+        rowv[0] = m1w;
+        *reinterpret_cast<double*>(rowv + 2) = ps;
+        rowu[0] = nc;
+        rowu[1] = (nan || !is_finite(m1w) || nc > (uint32_t)kCandCap) ? 1u : 0u;
+      }
+    }
+    __syncthreads();
+    m1 = rowv[0];
+    const double p_slice = *reinterpret_cast<const double*>(rowv + 2);
+    const uint32_t cbase = rowu[2];
+    bad = !ok || rowu[1] != 0u;
+    __syncthreads();
+    if (bad) break;
+    float* hg = a.hist + ((uint64_t)b * kMaxSlices + vs) * kMassBins;
     // Candidates in index order at the slice's block: (logit bits << 32) |
     // id, and exp(v - m1) in the second half of the buffer; their exp-mass
     // binned by the bits of exp(v - m1) into this slice's histogram (bin 0
@@ -485,12 +536,12 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     for (uint32_t i = t; i < kBins; i += kThreads) hl[i] = 0.f;
     // the exact summands exp(v - m1), into this thread's LDS row
 #pragma unroll
-    for (int q = 0; q < (int)kResK / 4; ++q) {
-      const float e0 = expf_glibc_nonpos(__fsub_rn(x[4 * q], m1));
-      const float e1 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 1], m1));
-      const float e2 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 2], m1));
-      const float e3 = expf_glibc_nonpos(__fsub_rn(x[4 * q + 3], m1));
-      *reinterpret_cast<float4*>(Lt + 4 * q) = make_float4(e0, e1, e2, e3);
+    for (int qq = 0; qq < (int)kResK / 4; ++qq) {
+      const float e0 = expf_glibc_nonpos(__fsub_rn(x[4 * qq], m1));
+      const float e1 = expf_glibc_nonpos(__fsub_rn(x[4 * qq + 1], m1));
+      const float e2 = expf_glibc_nonpos(__fsub_rn(x[4 * qq + 2], m1));
+      const float e3 = expf_glibc_nonpos(__fsub_rn(x[4 * qq + 3], m1));
+      *reinterpret_cast<float4*>(Lt + 4 * qq) = make_float4(e0, e1, e2, e3);
     }
     LUMEN_TICK("rb_exps", b);
 #ifdef LUMEN_RES_STOP
@@ -517,16 +568,20 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     for (uint32_t i = t; i < kBins; i += kThreads) hg[i] = hl[i];
     LUMEN_TICK("rb_hist", b);
     const uint32_t nthr = (sc.hi - sc.lo + kResK - 1u) / kResK;
-    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, sl), s);
+    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, vs), s);
     if (t == 0) {
-      ws.part_nrec[sl] = rc.ok ? rc.items : 0xffffffffu;
-      ws.part_nraw[sl] = rc.raws;
+      ws.part_nrec[vs] = rc.ok ? rc.items : 0xffffffffu;
+      ws.part_nraw[vs] = rc.raws;
     }
+    __syncthreads();
   }
+  const uint32_t ncand = s.H0[1032];
+  if (bad && t == 0) __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("r_phaseB", b);
   if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) return;
   LUMEN_TICK("r_finisher", b);
   RES_STOP(3);
+  G = Gv;  // from here on, slices are the virtual slices
 
   // ---- finisher ----
   // per-slice record sizes (one slice per lane of wave 0)

@@ -39,12 +39,24 @@ enum RowPath { kPathGreedy, kPathTopK, kPathTopP, kPathSingle };
 constexpr uint32_t kWgThreads = 1024;  // lumen_sample_rows workgroup size
 constexpr uint32_t kResSlice = 32u * kWgThreads;  // logits per register-resident slice
 
+// Chunks per workgroup of a register-resident row with G workgroups (the
+// kernel's res_chunks): the fewest q <= 4 with G * q <= kMaxSlices whose
+// G * q slices each hold at most kResSlice logits; 0 when none does.
+uint32_t res_chunks(uint32_t V, uint32_t G) {
+  for (uint32_t q = 1; q <= 4u && G * q <= (uint32_t)lumen::kMaxSlices; ++q)
+    if ((((V + G * q - 1u) / (G * q) + 15u) & ~15u) <= kResSlice) return q;
+  return 0u;
+}
+
 RowPath row_path(const RowParams& r, uint32_t V, uint32_t G) {
   if (r.flags & lumen::kGreedy) return kPathGreedy;
-  if ((r.flags & lumen::kTopK) && r.top_k <= 2048u) return kPathTopK;
+  if ((r.flags & lumen::kTopK) && r.top_k <= lumen::kTopKSplitMax) return kPathTopK;
   const uint32_t per = G ? ((V + G - 1u) / G + 15u) & ~15u : V;
-  // register-resident top-p slices (any penalties, min-p, temperature)
-  if ((r.flags & lumen::kTopP) && !(r.flags & lumen::kTopK) && per <= kResSlice) return kPathTopP;
+  // register-resident rows: top-p (any penalties, min-p, temperature), and
+  // plain temperature rows (no top-k, top-p or min-p)
+  if (!(r.flags & lumen::kTopK) && ((r.flags & lumen::kTopP) || !(r.flags & lumen::kMinP)) &&
+      V >= 64u && G > 1u && res_chunks(V, G) != 0u)
+    return kPathTopP;
   if ((r.flags & lumen::kTopP) && !(r.flags & (lumen::kTopK | lumen::kPen)) &&
       per <= 32u * kWgThreads * (uint32_t)lumen::kChainMaxQ)
     return kPathTopP;
@@ -90,9 +102,12 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
     wsum += w[b];
   }
   const uint32_t spare = cap > fixed ? cap - fixed : 0;
-  // fewest slices that keep a top-p row on the register-resident path
+  // fewest slices that keep a register-resident row at one chunk per
+  // workgroup; with up to 4 chunks per workgroup it may go down to a quarter
   uint32_t g_res = 1;
   while (g_res < lumen::kMaxSlices && ((V + g_res - 1u) / g_res + 15u) / 16u * 16u > kResSlice) ++g_res;
+  uint32_t g_min = std::max<uint32_t>(2u, (g_res + 3u) / 4u);
+  while (g_min < g_res && res_chunks(V, g_min) == 0u) ++g_min;
   std::vector<uint8_t> res(B, 0);
   uint64_t used = 0;
   for (uint32_t b = 0; b < B; ++b) {
@@ -100,17 +115,18 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
     uint64_t g = wsum ? ((uint64_t)spare * w[b] + wsum / 2) / wsum : 1;
     G[b] = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(g, lumen::kMaxSlices));
     const RowParams& r = rows[b];
-    res[b] = (r.flags & lumen::kTopP) && !(r.flags & (lumen::kTopK | lumen::kGreedy)) ? 1 : 0;
+    res[b] = !(r.flags & (lumen::kTopK | lumen::kGreedy)) &&
+                     ((r.flags & lumen::kTopP) || !(r.flags & lumen::kMinP)) ? 1 : 0;
     if (res[b] && G[b] < g_res) G[b] = g_res;
     if (row_path(rows[b], V, G[b]) == kPathSingle) G[b] = 1;
     used += G[b];
   }
-  // raising top-p rows to g_res may overrun the spare workgroups: take them
-  // back from the rows with the most slices, keeping top-p rows at g_res
+  // raising resident rows to g_res may overrun the spare workgroups: take
+  // them back from the rows with the most slices, resident rows down to g_min
   while (used > spare) {
     uint32_t pick = B;
     for (uint32_t b = 0; b < B; ++b) {
-      const uint32_t floor = res[b] ? g_res : 1u;
+      const uint32_t floor = res[b] ? g_min : 1u;
       if (G[b] > floor && (pick == B || G[b] > G[pick])) pick = b;
     }
     if (pick == B) break;  // every row at its floor: the XCD packing below trims

@@ -2485,7 +2485,8 @@ __device__ __forceinline__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem
 // list_push, to the row's global buffer with a single atomic. The count is
 // always added in full, so an overflow (of LDS or of the buffer) shows up as
 // a total above the capacity.
-__device__ __forceinline__ void flush_candidates(uint64_t* cand, uint32_t* gcnt, Smem& s) {
+__device__ __forceinline__ void flush_candidates(uint64_t* cand, uint32_t* gcnt, Smem& s,
+                                                 uint32_t cap = (uint32_t)kCandCap) {
   __syncthreads();
   const uint32_t n = s.cnt;
   if (threadIdx.x == 0)
@@ -2494,7 +2495,7 @@ __device__ __forceinline__ void flush_candidates(uint64_t* cand, uint32_t* gcnt,
   const uint32_t base = s.misc_u[1];
   const uint32_t m = min(n, (uint32_t)kCap);
   for (uint32_t j = threadIdx.x; j < m; j += kThreads)
-    if (base + j < (uint32_t)kCandCap) cand[base + j] = s.A[j];
+    if (base + j < cap) cand[base + j] = s.A[j];
   __syncthreads();
 }
 
@@ -2752,7 +2753,10 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     LUMEN_TICK("topk_sampled", b);
     if ((kDebugStop >> 8) == 1u) return;
   } else {
-    const uint32_t target = min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4));
+    // k up to 2048: 3k + 256 candidates; larger k use the whole row stride
+    // of the candidate buffer, aiming at 2.5k + 256
+    const uint32_t target = k <= 2048u ? min(3u * k + 256u, (uint32_t)(kCandCap * 3 / 4))
+                                       : min(5u * k / 2u + 256u, (uint32_t)kTopKCandCap * 3u / 4u);
     tau = sample_threshold(row, V, target, s);
     LUMEN_TICK("topk_sampled", b);
     if ((kDebugStop >> 8) == 1u) return;
@@ -2781,21 +2785,23 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
       list_push(s.A, &s.cnt, in, ((uint64_t)(~kk) << 32) | id);
     }
   }
-  flush_candidates(cand, &ws.cand_n, s);
+  flush_candidates(cand, &ws.cand_n, s, kTopKCandCap);
   LUMEN_TICK("topk_compacted", b);
   if ((kDebugStop >> 8) == 2u) return;
   const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
   if (old != G - 1u) return;
   LUMEN_TICK("topk_finisher", b);
   const uint32_t n = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (n < k || n > (uint32_t)kCandCap) {
+  if (n < k || n > kTopKCandCap) {
     row_single(a, b, s);
     return;
   }
   RowTrace tr;
   init_trace(tr, V);
   tr.passes = 1;
-  for (uint32_t j = threadIdx.x; j < n; j += kThreads) s.A[j] = cand[j];
+  // up to kTopKCandCap entries: list A continues into list B (adjacent)
+  uint64_t* const CL = s.A;
+  for (uint32_t j = threadIdx.x; j < n; j += kThreads) CL[j] = cand[j];
   __syncthreads();
   LUMEN_TICK("topk_loaded", b);
   if ((kDebugStop >> 8) == 3u) {
@@ -2803,24 +2809,26 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     return;
   }
   // candidate entries are (~key << 32) | idx
-  auto ckey = [&](uint32_t j) { return ~(uint32_t)(s.A[j] >> 32); };
+  auto ckey = [&](uint32_t j) { return ~(uint32_t)(CL[j] >> 32); };
   uint32_t cut, ns;
   if (k == 1) {
     // sampling.rs:913-921: exactly the lowest-index maximum
     uint64_t best = 0;
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) {
-      const uint64_t e = s.A[j];
+      const uint64_t e = CL[j];
       const uint64_t kk = ((uint64_t)(~(uint32_t)(e >> 32)) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
       best = kk > best ? kk : best;
     }
     best = block_max_u64(best, s);
     cut = (uint32_t)(best >> 32);
-    if (threadIdx.x == 0) s.Bk[0] = ((uint64_t)(0xffffffffu - (uint32_t)best) << 32) | cut;
+    if (threadIdx.x == 0) s.A[0] = ((uint64_t)(0xffffffffu - (uint32_t)best) << 32) | cut;
     ns = 1;
     __syncthreads();
   } else {
     cut = select_desc(n, ckey, k - 1u, s);
-    // survivors (every key >= cut, ties included) as (idx << 32) | key
+    // survivors (every key >= cut, ties included) as (idx << 32) | key,
+    // compacted in place: a chunk's entries are all read before any write,
+    // and a survivor never moves past its own position
     if (threadIdx.x == 0) s.cnt = 0;
     __syncthreads();
     for (uint32_t base = 0; base < n; base += kThreads) {
@@ -2830,20 +2838,24 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
       if (j < n) {
         const uint32_t kk = ckey(j);
         in = kk >= cut;
-        e = ((uint64_t)(uint32_t)s.A[j] << 32) | kk;
+        e = ((uint64_t)(uint32_t)CL[j] << 32) | kk;
       }
-      list_push(s.Bk, &s.cnt, in, e);
+      __syncthreads();
+      list_push(CL, &s.cnt, in, e);
     }
     __syncthreads();
     ns = s.cnt;
+    if (ns > (uint32_t)kCap) {
+      // more tied survivors than a list holds
+      row_single(a, b, s);
+      return;
+    }
   }
   LUMEN_TICK("topk_sort1", b);
   if ((kDebugStop >> 8) == 4u) {
     if (threadIdx.x == 0) a.tokens[b] = 0u;
     return;
   }
-  for (uint32_t j = threadIdx.x; j < ns; j += kThreads) s.A[j] = s.Bk[j];
-  __syncthreads();
   sort_u64_asc(s.A, ns, s.Bk, s);  // ascending index
   tr.topk_cutoff_key = cut;
   tr.topk_survivors = ns;
@@ -3554,6 +3566,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
 }  // namespace lumen
 
 #include "resident.h"
+#include "plain.h"
 
 namespace lumen {
 
@@ -3634,14 +3647,33 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
         greedy_guard_split(a, (int)b, sl, G, s);
       else
         greedy_split(a, (int)b, sl, G, s);
-    } else if ((flags & kTopK) && top_k <= 2048u) {
+    } else if ((flags & kTopK) && top_k <= kTopKSplitMax) {
       topk_split(a, (int)b, sl, G, s);
-    } else if ((flags & kTopP) && !(flags & kTopK) && per <= kResSlice && a.vocab >= 64u &&
-               make_row(a, (int)b).vec) {
-      if (a.dtype == 0)
-        topp_res<false>(a, (int)b, sl, G, s);
-      else
-        topp_res<true>(a, (int)b, sl, G, s);
+    } else if (!(flags & kTopK) && ((flags & kTopP) || !(flags & kMinP)) && a.vocab >= 64u &&
+               make_row(a, (int)b).vec && res_chunks(a.vocab, G) != 0u) {
+      // register-resident rows: top-p, or plain temperature
+      const uint32_t q = res_chunks(a.vocab, G);
+      if (flags & kTopP) {
+        if (q == 1u) {
+          if (a.dtype == 0)
+            topp_res<false, false>(a, (int)b, sl, G, q, s);
+          else
+            topp_res<true, false>(a, (int)b, sl, G, q, s);
+        } else if (a.dtype == 0) {
+          topp_res<false, true>(a, (int)b, sl, G, q, s);
+        } else {
+          topp_res<true, true>(a, (int)b, sl, G, q, s);
+        }
+      } else if (q == 1u) {
+        if (a.dtype == 0)
+          temp_res<false, false>(a, (int)b, sl, G, q, s);
+        else
+          temp_res<true, false>(a, (int)b, sl, G, q, s);
+      } else if (a.dtype == 0) {
+        temp_res<false, true>(a, (int)b, sl, G, q, s);
+      } else {
+        temp_res<true, true>(a, (int)b, sl, G, q, s);
+      }
     } else if ((flags & kTopP) && !(flags & (kTopK | kPen)) &&
                per <= 32u * kThreads * kChainMaxQ) {
       topp_split(a, (int)b, sl, G, s);

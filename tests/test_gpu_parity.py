@@ -463,6 +463,36 @@ def test_config5_full(eng):
     _run_workload(eng, config5())
 
 
+def test_defaults_full(eng):
+    # the parameter sets callers send most: the reference default (T 1.0
+    # alone), the server default without top_p (T 0.7, repetition 1.05), that
+    # with top_p 0.9, and min_p + top_p + top_k 4,096, at full vocabulary
+    from lumen_amd.workloads import defaults
+
+    _run_workload(eng, defaults())
+
+
+def test_plain_temperature_rows(eng):
+    # plain temperature rows (no top-k / top-p / min-p) over several batch
+    # shapes and temperatures, f32 and bf16, with and without penalties
+    rng = np.random.default_rng(77)
+    for B, V, dt in ((4, 248_320, "f32"), (16, 151_936, "bf16"), (64, 131_072, "f32"),
+                     (8, 32_768, "f32")):
+        lg = (rng.normal(0, 2.0, (B, V)) + rng.gumbel(0, 1, (B, V))).astype(np.float32)
+        params = [SP(temperature=float(rng.choice([0.3, 0.7, 1.0, 1.3])),
+                     repetition_penalty=(1.1 if b % 2 else None),
+                     frequency_penalty=(0.4 if b % 3 == 0 else None)) for b in range(B)]
+        hists = [rng.integers(0, V, int(rng.integers(0, 3000))).astype(np.uint32) for _ in range(B)]
+        u = rng.random(B).astype(np.float32)
+        if dt == "bf16":
+            bits = (lg.view(np.uint32) >> 16).astype(np.uint16)
+            lg = (bits.astype(np.uint32) << 16).view(np.float32)
+            rep = parity.compare(eng, lg, params, hists, u, dtype="bf16", bf16_bits=bits)
+        else:
+            rep = parity.compare(eng, lg, params, hists, u, check_pen=True)
+        assert_clean(rep, f"plain B={B} V={V} {dt}")
+
+
 def test_config4_full(eng):
     # B=256 bf16 rows over a flat distribution with top_p 0.99: the nucleus
     # spans most of the vocabulary (the sort / prefix-sum worst case)
