@@ -32,183 +32,6 @@
 
 namespace lumen {
 
-// The records of the row's G slices gathered into LDS (s.Bk as words): items
-// of slice i from ib[i], raw slots of slice i from rb[i] (ib, rb in s.H0 +
-// [0, 64)); returns false when they do not fit or a slice failed to record.
-__device__ __forceinline__ bool res_gather(const KernelArgs& a, int b, uint32_t G, Smem& s,
-                                           uint32_t* nit_out, uint32_t* rawbase_out) {
-  RowWs& ws = a.ws[b];
-  const uint32_t t = threadIdx.x, lane = t & 63u;
-  uint32_t* ib = s.H0;
-  uint32_t* rb = s.H0 + 32;
-  if (t < 64u) {
-    const bool in = lane < G;
-    const uint32_t ni = in ? ws.part_nrec[lane] : 0u;
-    const uint32_t nr = in ? ws.part_nraw[lane] : 0u;
-    const bool failed = __ballot(in && ni == 0xffffffffu) != 0ull;
-    const uint32_t ei = wave_scan_incl(failed ? 0u : ni, 0u, op_add_u32);
-    const uint32_t er = wave_scan_incl(nr, 0u, op_add_u32);
-    const uint32_t pi = wave_shr1(ei, 0u), pr = wave_shr1(er, 0u);
-    if (lane <= G) {
-      ib[lane] = pi;
-      rb[lane] = pr;
-    }
-    if (lane == 0) s.misc_u[3] = failed ? 1u : 0u;
-  }
-  __syncthreads();
-  const uint32_t nit = ib[G], nrw = rb[G];
-  const uint32_t rawbase = 4u * nit;
-  const uint32_t nw = rawbase + kResK * nrw;
-  const bool ok = s.misc_u[3] == 0u && nw <= 2u * (uint32_t)kCap;
-  __syncthreads();
-  if (!ok) return false;
-  uint32_t* words = reinterpret_cast<uint32_t*>(s.Bk);
-  auto src_of = [&](uint32_t f) -> const uint32_t* {
-    uint32_t i = 0;
-    if (f < rawbase) {
-      const uint32_t it = f >> 2;
-      while (i + 1u < G && ib[i + 1] <= it) ++i;
-      return res_rec(a, b, i) + 4u * (it - ib[i]) + (f & 3u);
-    }
-    const uint32_t r = (f - rawbase) / kResK;
-    while (i + 1u < G && rb[i + 1] <= r) ++i;
-    return res_rec(a, b, i) + kResRawOff + kResK * (r - rb[i]) + (f - rawbase) % kResK;
-  };
-  for (uint32_t f0 = 0; f0 < nw; f0 += 4u * kThreads) {
-    uint32_t wv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t f = f0 + t + (uint32_t)q * kThreads;
-      wv[q] = f < nw ? *src_of(f) : 0u;
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t f = f0 + t + (uint32_t)q * kThreads;
-      if (f < nw) words[f] = wv[q];
-    }
-  }
-  __syncthreads();
-  *nit_out = nit;
-  *rawbase_out = rawbase;
-  return true;
-}
-
-// Walk of the gathered records on wave 0 from a running sum of 0.
-//  sum mode (FIND false): the exact total; starts[i] (LDS) receives the exact
-//    running sum at the start of slice i.
-//  find mode: the first element whose running sum exceeds r (strictly,
-//    sampling.rs:1008-1011); it must lie in a raw (the records made every
-//    thread that may hold it uncertain).
-// Results in s.misc_u / s.red_f: [0] good, [1] found, [2] item, [3] element
-// in the raw; red_f[0] final or hit sum, red_f[1] the sum before the hit.
-template <bool FIND>
-__device__ __forceinline__ void res_walk(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
-                                         float* starts, Smem& s) {
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t* ib = s.H0;
-  const uint32_t* rb = s.H0 + 32;
-  const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
-  const uint4* items = reinterpret_cast<const uint4*>(words);
-  const float* raws = reinterpret_cast<const float*>(words + rawbase);
-  uint32_t cb = 0u;
-  uint32_t good = 1, found = 0, hit_k = 0, hit_j = 0, before = 0u;
-  uint32_t ns = 0;  // next slice whose start is still to be recorded
-  for (uint32_t k0 = 0; k0 < nit && good && !found; k0 += 64u) {
-    const uint32_t k = k0 + lane;
-    uint4 it = make_uint4(0u, 0u, 0u, kNoRaw);
-    uint32_t roff = kNoRaw;
-    if (k < nit) {
-      it = items[k];
-      if (it.w != kNoRaw) {
-        uint32_t i = 0;
-        while (i + 1u < G && ib[i + 1] <= k) ++i;
-        roff = kResK * (rb[i] + (it.w & 0xffffu));
-      }
-    }
-    const uint32_t cnt = min(64u, nit - k0);
-    for (uint32_t q = 0; q < cnt; ++q) {
-      if (!FIND) {
-        while (ns < G && ib[ns] <= k0 + q) {
-          if (lane == 0) starts[ns] = __uint_as_float(cb);
-          ++ns;
-        }
-      }
-      const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
-      const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
-      const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
-      const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
-      const uint32_t inc = (cb & 1u) ? a1 : a0;
-      if (ro == kNoRaw) {
-        if ((cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u) {
-          // a run: the crossing cannot lie in it
-          if (FIND && r < __uint_as_float(cb + inc)) {
-            good = 0;
-            break;
-          }
-          cb += inc;
-        } else {
-          good = 0;
-          break;
-        }
-        continue;
-      }
-      // an uncertain thread: its map when the exact sum is inside its binade
-      // and stays there (and, searching, stays at or below r), else its raw
-      // summands from the exact start
-      if ((cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u &&
-          !(FIND && r < __uint_as_float(cb + inc))) {
-        cb += inc;
-        continue;
-      }
-      const float4* r4 = reinterpret_cast<const float4*>(raws + ro);
-      float4 f[kResK / 4];
-#pragma unroll
-      for (int m = 0; m < (int)kResK / 4; ++m) f[m] = r4[m];
-      float c = __uint_as_float(cb);
-      uint32_t hj = kResK;
-      float cbef = c;
-#pragma unroll
-      for (int m = 0; m < (int)kResK / 4; ++m) {
-        const float xq[4] = {f[m].x, f[m].y, f[m].z, f[m].w};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float y = __fadd_rn(c, xq[u]);
-          if (FIND && hj == kResK && r < y) {
-            hj = 4u * (uint32_t)m + (uint32_t)u;
-            cbef = c;
-          }
-          c = y;
-        }
-      }
-      if (FIND && hj < kResK) {
-        // recompute the hit sum (the loop ran past it)
-        const float hit = __fadd_rn(cbef, reinterpret_cast<const float*>(r4)[hj]);
-        found = 1;
-        hit_k = k0 + q;
-        hit_j = hj;
-        before = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(cbef));
-        cb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(hit));
-        break;
-      }
-      cb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(c));
-    }
-  }
-  if (!FIND && good) {
-    while (ns < G) {
-      if (lane == 0) starts[ns] = __uint_as_float(cb);
-      ++ns;
-    }
-  }
-  if (lane == 0) {
-    s.misc_u[0] = good;
-    s.misc_u[1] = found;
-    s.misc_u[2] = hit_k;
-    s.misc_u[3] = hit_j;
-    s.red_f[0] = __uint_as_float(cb);
-    s.red_f[1] = __uint_as_float(before);
-  }
-}
-
 // Plain temperature sampling over register-resident slices; see the header
 // comment. Workgroup sl owns the q virtual slices sl*q .. sl*q+q-1 of the
 // row's G*q (res_chunks); with q > 1 each is read again (from cache) in the

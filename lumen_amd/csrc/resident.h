@@ -333,6 +333,183 @@ __device__ __forceinline__ uint32_t res_sample_select(const float (&smp)[4], uin
   return tau;
 }
 
+// The records of the row's G slices gathered into LDS (s.Bk as words): items
+// of slice i from ib[i], raw slots of slice i from rb[i] (ib, rb in s.H0 +
+// [0, 64)); returns false when they do not fit or a slice failed to record.
+__device__ __forceinline__ bool res_gather(const KernelArgs& a, int b, uint32_t G, Smem& s,
+                                           uint32_t* nit_out, uint32_t* rawbase_out) {
+  RowWs& ws = a.ws[b];
+  const uint32_t t = threadIdx.x, lane = t & 63u;
+  uint32_t* ib = s.H0;
+  uint32_t* rb = s.H0 + 32;
+  if (t < 64u) {
+    const bool in = lane < G;
+    const uint32_t ni = in ? ws.part_nrec[lane] : 0u;
+    const uint32_t nr = in ? ws.part_nraw[lane] : 0u;
+    const bool failed = __ballot(in && ni == 0xffffffffu) != 0ull;
+    const uint32_t ei = wave_scan_incl(failed ? 0u : ni, 0u, op_add_u32);
+    const uint32_t er = wave_scan_incl(nr, 0u, op_add_u32);
+    const uint32_t pi = wave_shr1(ei, 0u), pr = wave_shr1(er, 0u);
+    if (lane <= G) {
+      ib[lane] = pi;
+      rb[lane] = pr;
+    }
+    if (lane == 0) s.misc_u[3] = failed ? 1u : 0u;
+  }
+  __syncthreads();
+  const uint32_t nit = ib[G], nrw = rb[G];
+  const uint32_t rawbase = 4u * nit;
+  const uint32_t nw = rawbase + kResK * nrw;
+  const bool ok = s.misc_u[3] == 0u && nw <= 2u * (uint32_t)kCap;
+  __syncthreads();
+  if (!ok) return false;
+  uint32_t* words = reinterpret_cast<uint32_t*>(s.Bk);
+  auto src_of = [&](uint32_t f) -> const uint32_t* {
+    uint32_t i = 0;
+    if (f < rawbase) {
+      const uint32_t it = f >> 2;
+      while (i + 1u < G && ib[i + 1] <= it) ++i;
+      return res_rec(a, b, i) + 4u * (it - ib[i]) + (f & 3u);
+    }
+    const uint32_t r = (f - rawbase) / kResK;
+    while (i + 1u < G && rb[i + 1] <= r) ++i;
+    return res_rec(a, b, i) + kResRawOff + kResK * (r - rb[i]) + (f - rawbase) % kResK;
+  };
+  for (uint32_t f0 = 0; f0 < nw; f0 += 4u * kThreads) {
+    uint32_t wv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t f = f0 + t + (uint32_t)q * kThreads;
+      wv[q] = f < nw ? *src_of(f) : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t f = f0 + t + (uint32_t)q * kThreads;
+      if (f < nw) words[f] = wv[q];
+    }
+  }
+  __syncthreads();
+  *nit_out = nit;
+  *rawbase_out = rawbase;
+  return true;
+}
+
+// Walk of the gathered records on wave 0 from a running sum of 0.
+//  sum mode (FIND false): the exact total; starts[i] (LDS) receives the exact
+//    running sum at the start of slice i.
+//  find mode: the first element whose running sum exceeds r (strictly,
+//    sampling.rs:1008-1011); it must lie in a raw (the records made every
+//    thread that may hold it uncertain).
+// Results in s.misc_u / s.red_f: [0] good, [1] found, [2] item, [3] element
+// in the raw; red_f[0] final or hit sum, red_f[1] the sum before the hit.
+template <bool FIND>
+__device__ __forceinline__ void res_walk(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
+                                         float* starts, Smem& s) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t* ib = s.H0;
+  const uint32_t* rb = s.H0 + 32;
+  const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
+  const uint4* items = reinterpret_cast<const uint4*>(words);
+  const float* raws = reinterpret_cast<const float*>(words + rawbase);
+  uint32_t cb = 0u;
+  uint32_t good = 1, found = 0, hit_k = 0, hit_j = 0, before = 0u;
+  uint32_t ns = 0;  // next slice whose start is still to be recorded
+  for (uint32_t k0 = 0; k0 < nit && good && !found; k0 += 64u) {
+    const uint32_t k = k0 + lane;
+    uint4 it = make_uint4(0u, 0u, 0u, kNoRaw);
+    uint32_t roff = kNoRaw;
+    if (k < nit) {
+      it = items[k];
+      if (it.w != kNoRaw) {
+        uint32_t i = 0;
+        while (i + 1u < G && ib[i + 1] <= k) ++i;
+        roff = kResK * (rb[i] + (it.w & 0xffffu));
+      }
+    }
+    const uint32_t cnt = min(64u, nit - k0);
+    for (uint32_t q = 0; q < cnt; ++q) {
+      if (!FIND && starts) {
+        while (ns < G && ib[ns] <= k0 + q) {
+          if (lane == 0) starts[ns] = __uint_as_float(cb);
+          ++ns;
+        }
+      }
+      const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
+      const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
+      const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
+      const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
+      const uint32_t inc = (cb & 1u) ? a1 : a0;
+      if (ro == kNoRaw) {
+        if ((cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u) {
+          // a run: the crossing cannot lie in it
+          if (FIND && r < __uint_as_float(cb + inc)) {
+            good = 0;
+            break;
+          }
+          cb += inc;
+        } else {
+          good = 0;
+          break;
+        }
+        continue;
+      }
+      // an uncertain thread: its map when the exact sum is inside its binade
+      // and stays there (and, searching, stays at or below r), else its raw
+      // summands from the exact start
+      if ((cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u &&
+          !(FIND && r < __uint_as_float(cb + inc))) {
+        cb += inc;
+        continue;
+      }
+      const float4* r4 = reinterpret_cast<const float4*>(raws + ro);
+      float4 f[kResK / 4];
+#pragma unroll
+      for (int m = 0; m < (int)kResK / 4; ++m) f[m] = r4[m];
+      float c = __uint_as_float(cb);
+      uint32_t hj = kResK;
+      float cbef = c;
+#pragma unroll
+      for (int m = 0; m < (int)kResK / 4; ++m) {
+        const float xq[4] = {f[m].x, f[m].y, f[m].z, f[m].w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float y = __fadd_rn(c, xq[u]);
+          if (FIND && hj == kResK && r < y) {
+            hj = 4u * (uint32_t)m + (uint32_t)u;
+            cbef = c;
+          }
+          c = y;
+        }
+      }
+      if (FIND && hj < kResK) {
+        // recompute the hit sum (the loop ran past it)
+        const float hit = __fadd_rn(cbef, reinterpret_cast<const float*>(r4)[hj]);
+        found = 1;
+        hit_k = k0 + q;
+        hit_j = hj;
+        before = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(cbef));
+        cb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(hit));
+        break;
+      }
+      cb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(c));
+    }
+  }
+  if (!FIND && good && starts) {
+    while (ns < G) {
+      if (lane == 0) starts[ns] = __uint_as_float(cb);
+      ++ns;
+    }
+  }
+  if (lane == 0) {
+    s.misc_u[0] = good;
+    s.misc_u[1] = found;
+    s.misc_u[2] = hit_k;
+    s.misc_u[3] = hit_j;
+    s.red_f[0] = __uint_as_float(cb);
+    s.red_f[1] = __uint_as_float(before);
+  }
+}
+
 // Loads virtual slice sc into x (thread t: elements 32t .. 32t+31) with the
 // penalties applied (sampling.rs:881-900, each history id once). The loads
 // v must have been issued for sc (res_issue).
@@ -366,6 +543,33 @@ __device__ __forceinline__ uint32_t res_chunks(uint32_t V, uint32_t G) {
   for (uint32_t q = 1; q <= 4u && G * q <= (uint32_t)kMaxSlices; ++q)
     if ((((V + G * q - 1u) / (G * q) + 15u) & ~15u) <= kResSlice) return q;
   return 0u;
+}
+
+// The second-to-last workgroup of a split top-p row to arrive: it waits for
+// the last (every slice's records are then complete), walks the records of
+// the Gv virtual slices to the exact softmax sum S1 and publishes it in the
+// row's block (unused0), releasing it by raising the spin barrier from G to
+// 2G. On any failure it sets a status bit instead; it always releases, so
+// the finisher never waits past the timeout.
+__device__ __forceinline__ void res_s1_walker(const KernelArgs& a, int b, uint32_t G, uint32_t Gv,
+                                              Smem& s) {
+  RowWs& ws = a.ws[b];
+  const bool ok = wg_wait_geq(&ws.arrive, G, s);
+  uint32_t nit = 0, rawbase = 0;
+  bool good = ok && __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
+              res_gather(a, b, Gv, s, &nit, &rawbase);
+  if (good) {
+    if (threadIdx.x < 64u) res_walk<false>(Gv, nit, rawbase, 0.f, nullptr, s);
+    __syncthreads();
+    good = s.misc_u[0] != 0u;
+  }
+  if (threadIdx.x == 0) {
+    if (good)
+      ws.unused0 = __float_as_uint(s.red_f[0]);
+    else
+      __hip_atomic_fetch_or(&ws.status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(&ws.bar, G, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Top-p (no top-k) over register-resident slices; see the header comment.
@@ -578,63 +782,28 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   const uint32_t ncand = s.H0[1032];
   if (bad && t == 0) __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("r_phaseB", b);
-  if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) return;
+  const uint32_t arr = wg_arrive(&ws.arrive, G - 1u, s);
+  if (arr == G - 2u) {
+    res_s1_walker(a, b, G, Gv, s);
+    return;
+  }
+  if (arr != G - 1u) return;
   LUMEN_TICK("r_finisher", b);
   RES_STOP(3);
+  const uint32_t Gr = G;
   G = Gv;  // from here on, slices are the virtual slices
 
   // ---- finisher ----
-  // per-slice record sizes (one slice per lane of wave 0)
-  uint32_t* ib = s.H0;       // [G + 1] first item of each slice
-  uint32_t* rb = s.H0 + 32;  // [G + 1] first raw slot
-  if (t < 64u) {
-    const bool in = lane < G;
-    const uint32_t ni = in ? ws.part_nrec[lane] : 0u;
-    const uint32_t nr = in ? ws.part_nraw[lane] : 0u;
-    const bool failed = __ballot(in && ni == 0xffffffffu) != 0ull;
-    const uint32_t ei = wave_scan_incl(failed ? 0u : ni, 0u, op_add_u32);
-    const uint32_t er = wave_scan_incl(nr, 0u, op_add_u32);
-    const uint32_t pi = wave_shr1(ei, 0u), pr = wave_shr1(er, 0u);
-    if (lane <= G) {
-      ib[lane] = pi;
-      rb[lane] = pr;
-    }
-    if (lane == 0) s.misc_u[3] = failed ? 1u : 0u;
-  }
-  __syncthreads();
-  const uint32_t nit = ib[G], nrw = rb[G];
-  const uint32_t rawbase = 4u * nit;  // LDS word offset of the raws (s.Bk)
-  bad = bad || s.misc_u[3] != 0u || rawbase + kResK * nrw > 2u * (uint32_t)kCap ||
-        __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-  if (bad) {
-    row_single(a, b, s);
-    return;
-  }
-  // Gather, every load issued before any store (one round trip): the
-  // records (items, then raws) into s.Bk, the summed mass histogram into
-  // s.H, the candidates (logit bits << 32) | id into list A.
+  // The walker (res_s1_walker) computes the exact S1 meanwhile. Until it
+  // arrives, the window is planned with an upper bound of S1 and sorted by
+  // e = exp(v - m1), which orders the candidates as p = e / S1 does except
+  // among equal p (repaired below).
+  bad = bad || __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
   constexpr uint32_t kPer = (uint32_t)kCandCap / (uint32_t)kThreads;
+  // gather, every load issued before any store: the summed mass histogram
+  // into s.H, the candidates (logit bits << 32) | id into list A, and the
+  // upper bound of S1 from the slices' estimates
   {
-    uint32_t* words = reinterpret_cast<uint32_t*>(s.Bk);
-    const uint32_t nw = rawbase + kResK * nrw;
-    auto src_of = [&](uint32_t f) -> const uint32_t* {
-      uint32_t i = 0;
-      if (f < rawbase) {
-        const uint32_t it = f >> 2;
-        while (i + 1u < G && ib[i + 1] <= it) ++i;
-        return res_rec(a, b, i) + 4u * (it - ib[i]) + (f & 3u);
-      }
-      const uint32_t r = (f - rawbase) / kResK;
-      while (i + 1u < G && rb[i + 1] <= r) ++i;
-      return res_rec(a, b, i) + kResRawOff + kResK * (r - rb[i]) + (f - rawbase) % kResK;
-    };
-    constexpr int kWq = 4;
-    uint32_t wv[kWq];
-#pragma unroll
-    for (int q = 0; q < kWq; ++q) {
-      const uint32_t f = t + (uint32_t)q * kThreads;
-      wv[q] = f < nw ? *src_of(f) : 0u;
-    }
     uint64_t cv[kPer];
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
@@ -650,23 +819,15 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
 #pragma unroll
       for (uint32_t i = 0; i < (uint32_t)kMaxSlices; ++i) hs += hv[i];
     }
-    for (uint32_t f0 = kWq * kThreads; f0 < nw; f0 += kWq * kThreads) {  // long records (rare)
-      uint32_t xv[kWq];
-#pragma unroll
-      for (int q = 0; q < kWq; ++q) {
-        const uint32_t f = f0 + t + (uint32_t)q * kThreads;
-        xv[q] = f < nw ? *src_of(f) : 0u;
-      }
-#pragma unroll
-      for (int q = 0; q < kWq; ++q) {
-        const uint32_t f = f0 + t + (uint32_t)q * kThreads;
-        if (f < nw) words[f] = xv[q];
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kWq; ++q) {
-      const uint32_t f = t + (uint32_t)q * kThreads;
-      if (f < nw) words[f] = wv[q];
+    if (t < 64u) {
+      const bool in = lane < G;
+      const float mi = in ? ws.part_max[lane] : kNegInf;
+      const double ei = in ? ws.part_e[lane] : 0.0;
+      const double term = (in && mi != kNegInf) ? ei * exp((double)mi - (double)m1) : 0.0;
+      const double est = wave_reduce(term, 0.0, [](double l, double r) { return l + r; });
+      // the sequential f32 sum is within ~1e-3 of the estimate; the window's
+      // margin covers that, and the checks after the walk make it exact
+      if (lane == 0) s.red_f[2] = (float)est;
     }
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
@@ -678,79 +839,16 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   }
   LUMEN_TICK("r_gathered", b);
   RES_STOP(4);
-  // exact S1: the records in row order from 0, on wave 0; 64 items at a
-  // time sit in the lanes' registers, the walk reads them with readlane
-  if (t < 64u) {
-    const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
-    const uint4* items = reinterpret_cast<const uint4*>(words);
-    const float* raws = reinterpret_cast<const float*>(words + rawbase);
-    uint32_t cb = 0u;  // bits of the exact running sum
-    uint32_t good = 1;
-    for (uint32_t k0 = 0; k0 < nit && good; k0 += 64u) {
-      const uint32_t k = k0 + lane;
-      uint4 it = make_uint4(0u, 0u, 0u, kNoRaw);
-      uint32_t roff = kNoRaw;
-      if (k < nit) {
-        it = items[k];
-        if (it.w != kNoRaw) {
-          uint32_t i = 0;
-          while (i + 1u < G && ib[i + 1] <= k) ++i;
-          roff = kResK * (rb[i] + it.w);
-        }
-      }
-      const uint32_t cnt = min(64u, nit - k0);
-      for (uint32_t q = 0; q < cnt; ++q) {
-        const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
-        const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
-        const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
-        const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
-        const uint32_t inc = (cb & 1u) ? a1 : a0;
-        if ((cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u) {
-          cb += inc;
-        } else if (ro != kNoRaw) {
-          const float4* r4 = reinterpret_cast<const float4*>(raws + ro);
-          float4 f[kResK / 4];
-#pragma unroll
-          for (int m = 0; m < (int)kResK / 4; ++m) f[m] = r4[m];
-          float c = __uint_as_float(cb);
-#pragma unroll
-          for (int m = 0; m < (int)kResK / 4; ++m) {
-            c = __fadd_rn(c, f[m].x);
-            c = __fadd_rn(c, f[m].y);
-            c = __fadd_rn(c, f[m].z);
-            c = __fadd_rn(c, f[m].w);
-          }
-          cb = (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(c));
-        } else {
-          good = 0;
-          break;
-        }
-      }
-    }
-    if (lane == 0) {
-      s.red_f[0] = __uint_as_float(cb);
-      s.misc_u[3] = good;
-    }
-  }
-  __syncthreads();
-  const float S1 = s.red_f[0];
-  const bool walked = s.misc_u[3] != 0u;
-  __syncthreads();
-  LUMEN_TICK("r_S1", b);
-  RES_STOP(5);
-  if (!walked) {
-    row_single(a, b, s);
-    return;
-  }
+  const float S1_hi = s.red_f[2];
   // Window: the lowest mass bin (from the top) whose running mass reaches
   // top_p * S1 with a margin, plus one spare bin, bounds the window from
-  // below at p_lo. Every logit >= tv is a candidate, so every token with
-  // p > p(tv) is one: p_lo stays above p(tv).
+  // below at e_edge. Every logit >= tv is a candidate, so every token with
+  // e > e(tv) is one: the window keeps only e > e(tv).
   const float e_tv = tau ? expf_glibc_nonpos(__fsub_rn(tv, m1)) : 0.f;
   const uint32_t bsh = res_bin_shift(e_tv);
   if (t < 64u) {
     const float* hm = reinterpret_cast<const float*>(s.H);
-    const float target = fminf(__fmul_rn(__fmul_rn(P.top_p, S1), 1.004f), S1);
+    const float target = fminf(__fmul_rn(__fmul_rn(P.top_p, S1_hi), 1.004f), S1_hi);
     float run = 0.f;
     uint32_t hit = kBins;
     for (uint32_t base = 0; base < kBins && hit == kBins; base += 64u) {
@@ -762,60 +860,86 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     if (t == 0) s.misc_u[2] = hit;
   }
   __syncthreads();
-  float p_lo;
+  float e_lo;
   {
     const uint32_t hit = s.misc_u[2];
-    const float e_edge = hit + 1u < kBins ? res_bin_lo(hit + 1u, bsh) : 0.f;
-    p_lo = __fdiv_rn(fmaxf(e_edge, e_tv), S1);
-    if (tau) {
-      const float p_tv = __fdiv_rn(e_tv, S1);
-      if (!(p_lo > p_tv)) p_lo = __uint_as_float(__float_as_uint(p_tv) + 1u);
-    }
+    e_lo = fmaxf(hit + 1u < kBins ? res_bin_lo(hit + 1u, bsh) : 0.f, e_tv);
   }
-  // the window's sort keys (~p << 32) | f in list B (f, the candidate's
+  // the window's sort keys (~e << 32) | f in list B (f, the candidate's
   // position, orders like its id); candidates 8t .. 8t+7 per thread
   // (contiguous, so one block scan keeps index order)
   uint32_t wmask = 0;
-  float pj[kPer];
+  uint32_t ej[kPer];
   {
     const uint32_t* cande = reinterpret_cast<const uint32_t*>(cand + kCandCap);
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
       const uint32_t f = kPer * t + (uint32_t)q;
-      pj[q] = f < ncand ? __uint_as_float(cande[f]) : 0.f;
+      ej[q] = f < ncand ? cande[f] : 0u;
     }
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
-      pj[q] = __fdiv_rn(pj[q], S1);
-      wmask |= (pj[q] > 0.f && pj[q] >= p_lo ? 1u : 0u) << q;
+      const float e = __uint_as_float(ej[q]);
+      wmask |= (e > e_tv && e >= e_lo && e > 0.f ? 1u : 0u) << q;
     }
   }
   uint32_t nw;
   uint32_t wo = block_excl_scan_u32((uint32_t)__popc(wmask), s, &nw);
-  if (nw <= kResWindowCap) {
 #pragma unroll
-    for (int q = 0; q < (int)kPer; ++q)
-      if ((wmask >> q) & 1u) s.Bk[wo++] = ((uint64_t)(~__float_as_uint(pj[q])) << 32) | (kPer * t + (uint32_t)q);
-  }
+  for (int q = 0; q < (int)kPer; ++q)
+    if ((wmask >> q) & 1u) s.Bk[wo++] = ((uint64_t)(~ej[q]) << 32) | (kPer * t + (uint32_t)q);
   __syncthreads();
   LUMEN_TICK("r_window", b);
   RES_STOP(6);
-  if (nw > kResWindowCap || nw == 0u) {
-    row_single(a, b, s);
-    return;
-  }
-  {
-    const uint32_t khi = ~__float_as_uint(__fdiv_rn(1.0f, S1)), klo = ~__float_as_uint(p_lo);
+  // a window over half of list B sorts through list A (the candidates are
+  // then read again from the row's buffer)
+  const bool cand_lds = nw <= kResWindowCap;
+  uint64_t* const wtmp = cand_lds ? s.Bk + kResWindowCap : s.A;
+  if (!bad && nw > 0u) {
+    const uint32_t khi = ~__float_as_uint(1.0f), klo = ~__float_as_uint(e_lo);
     const uint64_t hint = ((uint64_t)(khi ^ klo) << 32) | span_mask(kCandCap);
-    sort_u64_asc(s.Bk, nw, s.Bk + kResWindowCap, s, hint);
+    sort_u64_asc(s.Bk, nw, wtmp, s, hint);
   }
   LUMEN_TICK("r_sorted", b);
   RES_STOP(7);
+  // S1 from the walker (always released, also on failure)
+  const bool got = wg_wait_geq(&ws.bar, 2u * Gr, s);
+  if (t == 0) {
+    s.misc_u[2] = __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s.red_f[0] = __uint_as_float(ws.unused0);
+  }
+  __syncthreads();
+  const float S1 = s.red_f[0];
+  bad = bad || !got || s.misc_u[2] != 0u;
+  __syncthreads();
+  LUMEN_TICK("r_S1", b);
+  if (bad || nw == 0u) {
+    row_single(a, b, s);
+    return;
+  }
+  // the keys as p = e / S1 (monotone in e, so the order holds), then the
+  // order among equal p repaired: (p desc, id asc) is the reference's
+  // stable sort (sampling.rs:952)
+  {
+    uint32_t swap = 0;
+    for (uint32_t j = t; j < nw; j += kThreads) {
+      const uint64_t k = s.Bk[j];
+      const float p = __fdiv_rn(__uint_as_float(~(uint32_t)(k >> 32)), S1);
+      s.Bk[j] = ((uint64_t)(~__float_as_uint(p)) << 32) | (uint32_t)k;
+    }
+    __syncthreads();
+    for (uint32_t j = t; j + 1u < nw; j += kThreads) swap |= s.Bk[j] > s.Bk[j + 1u] ? 1u : 0u;
+    swap = block_or_u32(swap, s);
+    if (swap) sort_u64_asc(s.Bk, nw, wtmp, s);
+  }
+  const float p_x = __fdiv_rn(e_lo, S1);  // every token outside the window has p <= p_x
   const EcssResult wk = list_ecss_block(
       nw, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe, P.top_p, 0.f, s);
   LUMEN_TICK("r_crossing", b);
   RES_STOP(8);
-  if (!wk.found) {
+  // the crossing's p must exceed every p outside the window, so no token
+  // outside it ties with (or precedes) the kept set
+  if (!wk.found || !(__uint_as_float(~(uint32_t)(s.Bk[wk.pos] >> 32)) > p_x)) {
     row_single(a, b, s);
     return;
   }
@@ -842,7 +966,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
       const bool in = (kmask >> q) & 1u;
-      cv[q] = in ? s.A[kPer * t + (uint32_t)q] : 0ull;
+      cv[q] = in ? (cand_lds ? s.A[kPer * t + (uint32_t)q] : cand[kPer * t + (uint32_t)q]) : 0ull;
       ev[q] = in && pre_exp ? cande[kPer * t + (uint32_t)q] : 0u;
     }
     uint32_t ko = block_excl_scan_u32((uint32_t)__popc(kmask), s, &nk);
@@ -861,7 +985,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   tr.topp_sum = S1;
   tr.topp_kept = (uint32_t)wk.pos + 1u;
   tr.topp_cum = wk.c;
-  tr.pad[0] = nit | (nrw << 16);
+  tr.pad[0] = 0;
   tr.pad[1] = ncand | (nw << 16);
   LUMEN_TICK("r_kept", b);
   RES_STOP(9);
