@@ -80,6 +80,7 @@ constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum c
 constexpr int kRowRecs = kMaxSlices * kChainMaxQ * 16;  // run records per row (one per wave segment)
 constexpr int kRecWords = 1152;     // words per run record slot
 
+
 // Per-row coordination block in device memory. Zero at allocation; the last
 // workgroup of a row to finish restores the counters to zero, so every
 // launch starts from a clean block.
@@ -186,5 +187,17 @@ struct KernelArgs {
   float inline_uniforms[kInlineRows];
   RowParams inline_params[kInlineRows];
 };
+
+// Stamp of the layouts the host library and the code object share. The
+// code object exports it (lumen_kernel_abi) and the library refuses a code
+// object whose stamp differs from its own: kernel arguments read with
+// another layout would be garbage pointers. kAbiVersion changes with any
+// change of meaning that keeps the sizes.
+constexpr uint32_t kAbiVersion = 3;
+constexpr uint32_t kAbiStamp =
+    (kAbiVersion * 0x9E3779B1u) ^ ((uint32_t)sizeof(KernelArgs) * 0x85EBCA77u) ^
+    ((uint32_t)sizeof(RowWs) * 0xC2B2AE3Du) ^ ((uint32_t)sizeof(RowParams) * 0x27D4EB2Fu) ^
+    ((uint32_t)sizeof(RowTrace) * 0x165667B1u) ^
+    ((uint32_t)kCandStride * 0xFD7046C5u) ^ ((uint32_t)kRowRecs * 0xB55A4F09u);
 
 }  // namespace lumen

@@ -403,12 +403,12 @@ __device__ __forceinline__ bool res_gather(const KernelArgs& a, int b, uint32_t 
 // Results in s.misc_u / s.red_f: [0] good, [1] found, [2] item, [3] element
 // in the raw; red_f[0] final or hit sum, red_f[1] the sum before the hit.
 template <bool FIND>
-__device__ __forceinline__ void res_walk(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
-                                         float* starts, Smem& s) {
+__device__ __forceinline__ void res_walk_at(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
+                                            const uint32_t* words, Smem& s,
+                                            float* starts = nullptr) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t* ib = s.H0;
   const uint32_t* rb = s.H0 + 32;
-  const uint32_t* words = reinterpret_cast<const uint32_t*>(s.Bk);
   const uint4* items = reinterpret_cast<const uint4*>(words);
   const float* raws = reinterpret_cast<const float*>(words + rawbase);
   uint32_t cb = 0u;
@@ -508,6 +508,13 @@ __device__ __forceinline__ void res_walk(uint32_t G, uint32_t nit, uint32_t rawb
     s.red_f[0] = __uint_as_float(cb);
     s.red_f[1] = __uint_as_float(before);
   }
+}
+
+// res_walk_at over the records gathered into s.Bk (res_gather).
+template <bool FIND>
+__device__ __forceinline__ void res_walk(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
+                                         float* starts, Smem& s) {
+  res_walk_at<FIND>(G, nit, rawbase, r, reinterpret_cast<const uint32_t*>(s.Bk), s, starts);
 }
 
 // Loads virtual slice sc into x (thread t: elements 32t .. 32t+31) with the

@@ -544,6 +544,21 @@ int lumen_sampler_create(lumen_sampler** out, int device) {
     delete s;
     return LUMEN_ERR_CODE_OBJECT;
   }
+  {
+    // a code object built from another layout of kernel_abi.h would read
+    // its arguments at the wrong offsets: refuse it
+    hipDeviceptr_t gp = nullptr;
+    size_t gsz = 0;
+    uint32_t stamp = 0;
+    const bool got = hipModuleGetGlobal(&gp, &gsz, s->module, "lumen_kernel_abi") == hipSuccess &&
+                     gsz == sizeof(uint32_t) && hipMemcpyDtoH(&stamp, gp, sizeof(stamp)) == hipSuccess;
+    if (!got || stamp != lumen::kAbiStamp) {
+      (void)hipGetLastError();
+      (void)hipModuleUnload(s->module);
+      delete s;
+      return fail(LUMEN_ERR_CODE_OBJECT, "code object built for another kernel ABI (rebuild it)");
+    }
+  }
   if (hipDeviceGetAttribute(&s->cu_count, hipDeviceAttributeMultiprocessorCount, device) !=
       hipSuccess)
     s->cu_count = 0;

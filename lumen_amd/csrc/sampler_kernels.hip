@@ -706,8 +706,10 @@ __device__ __forceinline__ EcssResult row_ecss(const Row& r, X&& xf, int mode, f
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[4 * q + j] = (i + j < V) ? xf(i + j, v[j]) : 0.f;
     }
+    LUMEN_TICK("ecss_x", LUMEN_TIMING_ROW);
     EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum,
                                       (int)min((uint32_t)kThreads, ((V - base) + (uint32_t)M - 1u) / (uint32_t)M));
+    LUMEN_TICK("ecss_chunk", LUMEN_TIMING_ROW);
     if (e.found) {
       e.pos += (int)base;
       return e;
@@ -823,8 +825,10 @@ __device__ __forceinline__ EcssResult const_ecss(uint32_t V, float u, int mode, 
     float x[M];
 #pragma unroll
     for (int j = 0; j < M; ++j) x[j] = (i0 + j < V) ? u : 0.f;
+    LUMEN_TICK("ecss_x", LUMEN_TIMING_ROW);
     EcssResult e = ecss_fast_chunk<M>(c, x, mode, theta, s.ecss, s.est, s.wsum,
                                       (int)min((uint32_t)kThreads, ((V - base) + (uint32_t)M - 1u) / (uint32_t)M));
+    LUMEN_TICK("ecss_chunk", LUMEN_TIMING_ROW);
     if (e.found) {
       e.pos += (int)base;
       return e;
@@ -1672,7 +1676,28 @@ __device__ __forceinline__ void bv_clear(Smem& s) {
 __device__ __forceinline__ void bv_count(float x, Smem& s) {
   const uint32_t pk = tkey(x) >> 16;
   atomicAdd(&bv_counts(s)[pk >> 1], 1u << ((pk & 1u) << 4));
-  atomicAdd(&s.H[pk >> 8], 1u);
+}
+
+// Per block of 256 values, the sum of the u16 counts into s.H[0 .. 255];
+// returns (uniformly) whether the counts are exact: a u16 count that
+// overflowed lost 65535 or 65536 (its carry goes to the neighbour or out of
+// the word), so the counts are exact iff they add up to the n elements
+// counted.
+__device__ __forceinline__ bool bv_blocks(uint32_t n, Smem& s) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t* cw = bv_counts(s);
+  uint32_t part = 0;  // values 64t .. 64t+63 (32 words)
+#pragma unroll 8
+  for (uint32_t i = 0; i < 32u; ++i) {
+    const uint32_t w = cw[32u * t + i];
+    part += (w & 0xffffu) + (w >> 16);
+  }
+  // 4 consecutive threads (lanes) hold one block of 256 values
+  uint32_t blk = part + __shfl_xor(part, 1);
+  blk += __shfl_xor(blk, 2);
+  if ((t & 3u) == 0u) s.H[t >> 2] = blk;
+  const uint32_t tot = block_sum_u32(part, s);
+  return tot == n;
 }
 
 // The value with key upper half pk: a negative value's key carries ones in
@@ -1689,15 +1714,21 @@ __device__ __forceinline__ float bv_value(uint32_t pk) {
 //   {x : key(x) >> 16 > pk_hi} + {x : pk_lo <= key(x) >> 16 <= pk_hi, id <= istar},
 // [pk_lo, pk_hi] being the values whose p equals the crossing's. Sets the
 // top-p trace fields. Uses s.A, s.Bk and s.H.
-template <class VF>
-__device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, float m1, float S1,
+// The row and the top-k mask (kmask: keys below kcut read as -inf) come by
+// value: in a non-inlined function, state reached through references would
+// be reloaded from private memory on every element.
+__device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask, uint32_t kcut,
+                                                       float m1, float S1,
                                                        float top_p, Smem& s, RowTrace& tr,
                                                        uint32_t& pk_lo, uint32_t& pk_hi,
                                                        uint32_t& istar) {
   const uint32_t t = threadIdx.x, V = row.V;
   const uint32_t* cw = bv_counts(s);
-  // a block of 256 values under 65536 occurrences bounds every u16 count
-  if (V > (1u << 22) || block_or_u32(t < 256u && s.H[t] > 0xffffu ? 1u : 0u, s)) return -1;
+  auto vf = [kmask, kcut](uint32_t, float v) -> float {
+    return (kmask && tkey(v) < kcut) ? kNegInf : v;
+  };
+  if (V > (1u << 22) || !bv_blocks(V, s)) return -1;
+  __syncthreads();
   auto pof = [&](uint32_t pk) { return __fdiv_rn(expf_glibc(__fsub_rn(bv_value(pk), m1)), S1); };
   if (t < 64u) {
     const uint32_t lane = t;
@@ -1707,6 +1738,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
     float ph = 0.f;
     for (int blk = 255; blk >= 0 && !h.found; --blk) {
       if (s.H[blk] == 0u) continue;
+      LUMEN_TICK("bv_blk", LUMEN_TIMING_ROW);
       for (int sub = 3; sub >= 0; --sub) {
         const uint32_t pk = (uint32_t)blk * 256u + (uint32_t)sub * 64u + (63u - lane);
         const uint32_t cnt = vcount(cw, pk);
@@ -1722,6 +1754,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
         rank += wave_reduce(cnt, 0u, op_add_u32);
       }
     }
+    LUMEN_TICK("bv_cross", LUMEN_TIMING_ROW);
     // the values around the crossing's with the same p (p is monotone in
     // the value, so they are adjacent among the values present)
     uint32_t hi = pks, lo = pks;
@@ -1762,7 +1795,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
   pk_hi = s.misc_u[3];
   tr.topp_cum = s.red_f[0];
   __syncthreads();
-  LUMEN_TICK("bv_walk", 0);
+  LUMEN_TICK("bv_walk", LUMEN_TIMING_ROW);
   if (!found) {
     tr.topp_kept = V;
     return 0;
@@ -1772,6 +1805,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
   uint32_t gt = 0;
   for (uint32_t pk = pk_hi + 1u + t; pk <= 0xffffu; pk += kThreads) gt += vcount(cw, pk);
   gt = block_sum_u32(gt, s);
+  LUMEN_TICK("bv_gt", LUMEN_TIMING_ROW);
   // the kept set ends at the (rank - gt)-th id, in id order, of the tokens
   // valued in [pk_lo, pk_hi]: an id histogram (lowest ids at the top) finds
   // its bin, then a bitmap of that bin its id
@@ -1786,10 +1820,12 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
   });
   __syncthreads();  // every wave's counts are in before the search reads them
   tr.passes++;
+  LUMEN_TICK("bv_idhist", LUMEN_TIMING_ROW);
   uint32_t ab = 0;
   const int d = find_from_top(s.H, 2048, k, &ab, s);
   const uint32_t lo = (2047u - (uint32_t)d) << sh, hi = min(V, lo + (1u << sh));
   const uint32_t kk = k - ab;
+  LUMEN_TICK("bv_find", LUMEN_TIMING_ROW);
   uint32_t* bits = s.H + 2048;  // one bit per id of the bin
   for (uint32_t i = t; i < 64u; i += kThreads) bits[i] = 0u;
   __syncthreads();
@@ -1815,7 +1851,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row& row, VF&& vf, 
   __syncthreads();
   istar = s.misc_u[2];
   __syncthreads();
-  LUMEN_TICK("bv_istar", 0);
+  LUMEN_TICK("bv_istar", LUMEN_TIMING_ROW);
   return 1;
 }
 
@@ -2058,14 +2094,16 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       tr.topp_sum = __uint_as_float(0x7fc00000u);
       tr.topp_kept = V;
     } else {
-      // softmax sum at T = 1 and a key histogram of the positive-probability tokens
+      // softmax sum at T = 1 and, for the window path, a key histogram of the
+      // positive-probability tokens (bf16 rows walk their value counts
+      // instead, and build it only if that walk cannot run)
       clear_hist(s.H0, 2048);
       __syncthreads();
       EcssResult e = row_ecss(
           row,
           [&](uint32_t i, float v) {
             float x = expf_glibc(__fsub_rn(v1f(v), m1));
-            if (x > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
+            if (!bf && x > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
             return x;
           },
           kEcssSum, 0.f, s);
@@ -2078,9 +2116,19 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       bool found = false;
       // bf16 rows: the walk over distinct values
       const int byval = !bf ? -1
-                            : topp_by_value(row, [&](uint32_t, float v) { return v1f(v); }, m1, S1,
-                                            P.top_p, s, tr, pk_lo, pk_hi, istar);
+                            : topp_by_value(row, kmask, kcut, m1, S1, P.top_p, s, tr, pk_lo, pk_hi,
+                                            istar);
       LUMEN_TICK("rs_byval", b);
+      if (bf && byval < 0) {
+        // the window path's key histogram, skipped above
+        clear_hist(s.H0, 2048);
+        __syncthreads();
+        row_foreach(row, [&](uint32_t i, float v) {
+          if (expf_glibc(__fsub_rn(v1f(v), m1)) > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
+        });
+        __syncthreads();
+        tr.passes++;
+      }
       if (byval >= 0) {
         tr.windows = 1;
         c = tr.topp_cum;
@@ -3613,6 +3661,9 @@ __device__ __forceinline__ void row_reset(const KernelArgs& a, uint32_t b, Smem&
     ws.status = 0;
   }
 }
+
+// The layout stamp the host library checks when it loads this code object.
+extern "C" __device__ __attribute__((used)) const uint32_t lumen_kernel_abi = kAbiStamp;
 
 extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs args) {
   // Device functions receive the arguments by reference. Referencing the

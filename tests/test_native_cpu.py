@@ -155,3 +155,16 @@ def test_device_expf_constants_match_oracle():
     for c in ("0x1.c6af84b912394p-5", "0x1.ebfce50fac4f3p-3", "0x1.62e42ff0c52d6p-1",
               "0x1.8p+52", "0x1.71547652b82fep+0", "0x1.62e42ep6f", "0x1.9fe368p6f"):
         assert c in dev and c in cpu, c
+
+
+def test_code_object_exports_abi_stamp():
+    # The library refuses a code object whose kernel-argument layout stamp
+    # differs from its own (sampler_host.cpp, lumen_sampler_create); the
+    # stamp is the exported symbol lumen_kernel_abi.
+    hsaco = os.path.join(ROOT, "lumen_amd", "lib", "lumen_sampler_gfx950.hsaco")
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not (os.path.exists(hsaco) and os.path.exists(readelf)):
+        pytest.skip("code object or llvm-readelf not present")
+    out = subprocess.run([readelf, "--symbols", hsaco], capture_output=True, text=True).stdout
+    line = [l for l in out.splitlines() if l.split() and l.split()[-1] == "lumen_kernel_abi"]
+    assert line and "OBJECT" in line[0]
