@@ -213,7 +213,7 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
     good = s.misc_u[0] != 0u;
   }
   if (!good) {
-    row_single(a, b, s);
+    row_single<false>(a, b, s);
     return;
   }
   const bool found = s.misc_u[1] != 0u;

@@ -921,7 +921,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   __syncthreads();
   LUMEN_TICK("r_S1", b);
   if (bad || nw == 0u) {
-    row_single(a, b, s);
+    row_single<false>(a, b, s);
     return;
   }
   // the keys as p = e / S1 (monotone in e, so the order holds), then the
@@ -947,7 +947,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   // the crossing's p must exceed every p outside the window, so no token
   // outside it ties with (or precedes) the kept set
   if (!wk.found || !(__uint_as_float(~(uint32_t)(s.Bk[wk.pos] >> 32)) > p_x)) {
-    row_single(a, b, s);
+    row_single<false>(a, b, s);
     return;
   }
   // the nucleus: the sorted window's first wk.pos + 1 entries, marked in a

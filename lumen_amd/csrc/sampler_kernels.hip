@@ -1900,8 +1900,16 @@ __device__ __forceinline__ uint32_t kth_id_where(const Row& row, VF&& vf, Pred&&
   return id;
 }
 
-// The whole sampler for row b, run by one workgroup (used directly when a
-// row has one workgroup, and as the fallback of the split paths).
+template <bool FIND, class XF>
+__device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, const Row& row,
+                                                  XF&& xf, float probe, Smem& s, bool& ok);
+
+// The whole sampler for row b, run by one workgroup: row_single<false> is the
+// fallback of the split paths inside lumen_sample_rows, row_single<true> the
+// body of lumen_sample_rows_single (one workgroup per row), whose full-row
+// exact sums take the record method (row_rec_sum). Two instantiations keep
+// the register allocation of the split kernel independent of the latter.
+template <bool V2>
 __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b, Smem& s) {
   const int t = threadIdx.x;
   const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
@@ -2097,16 +2105,23 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       // softmax sum at T = 1 and, for the window path, a key histogram of the
       // positive-probability tokens (bf16 rows walk their value counts
       // instead, and build it only if that walk cannot run)
-      clear_hist(s.H0, 2048);
-      __syncthreads();
-      EcssResult e = row_ecss(
-          row,
-          [&](uint32_t i, float v) {
-            float x = expf_glibc(__fsub_rn(v1f(v), m1));
-            if (!bf && x > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
-            return x;
-          },
-          kEcssSum, 0.f, s);
+      bool rec_ok = false;
+      EcssResult e{0.f, 0, -1, 0.f};
+      if (V2 && bf)
+        e = row_rec_sum<false>(a, b, row, [&](uint32_t, float v) { return expf_glibc(__fsub_rn(v1f(v), m1)); },
+                               0.f, s, rec_ok);
+      if (!rec_ok) {
+        clear_hist(s.H0, 2048);
+        __syncthreads();
+        e = row_ecss(
+            row,
+            [&](uint32_t i, float v) {
+              float x = expf_glibc(__fsub_rn(v1f(v), m1));
+              if (!bf && x > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
+              return x;
+            },
+            kEcssSum, 0.f, s);
+      }
       __syncthreads();
       tr.passes++;
       S1 = e.c;
@@ -2434,17 +2449,32 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
     tr.cdf_before = tr.cdf_at = __uint_as_float(0x7fc00000u);
     tok = V - 1;
   } else {
-    EcssResult S = row_ecss(
-        row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, kEcssSum,
-        0.f, s);
+    bool rec_ok = false;
+    EcssResult S{0.f, 0, -1, 0.f};
+    if (V2)
+      S = row_rec_sum<false>(
+          a, b, row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, 0.f, s,
+          rec_ok);
+    if (!rec_ok)
+      S = row_ecss(
+          row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, kEcssSum,
+          0.f, s);
     tr.passes++;
     LUMEN_TICK("rs_S3", b);
     const float S3 = S.c;
     tr.final_sum = S3;
-    EcssResult e = row_ecss(
-        row,
-        [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
-        kEcssFindGt, rdraw, s);
+    EcssResult e{0.f, 0, -1, 0.f};
+    rec_ok = false;
+    if (V2)
+      e = row_rec_sum<true>(
+          a, b, row,
+          [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
+          rdraw, s, rec_ok);
+    if (!rec_ok)
+      e = row_ecss(
+          row,
+          [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
+          kEcssFindGt, rdraw, s);
     tr.passes++;
     LUMEN_TICK("rs_cdf", b);
     tr.cdf_before = e.found ? e.before : e.c;
@@ -2841,7 +2871,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   LUMEN_TICK("topk_finisher", b);
   const uint32_t n = __hip_atomic_load(&ws.cand_n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (n < k || n > kTopKCandCap) {
-    row_single(a, b, s);
+    row_single<false>(a, b, s);
     return;
   }
   RowTrace tr;
@@ -2895,7 +2925,7 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     ns = s.cnt;
     if (ns > (uint32_t)kCap) {
       // more tied survivors than a list holds
-      row_single(a, b, s);
+      row_single<false>(a, b, s);
       return;
     }
   }
@@ -3437,7 +3467,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   LUMEN_TICK("p_finisher", b);
   if (!ok || single ||
       __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
-    row_single(a, b, s);
+    row_single<false>(a, b, s);
     return;
   }
   // Inputs from the other workgroups, fetched with as few dependent round
@@ -3589,7 +3619,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
     return;
   }
   if (!wk.found) {
-    row_single(a, b, s);
+    row_single<false>(a, b, s);
     return;
   }
   tr.windows = 1;
@@ -3615,6 +3645,7 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
 
 #include "resident.h"
 #include "plain.h"
+#include "rowsum.h"
 
 namespace lumen {
 
@@ -3685,7 +3716,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
   LUMEN_TICK_SLOT(b, sl);
   __syncthreads();
   if (G == 1u) {
-    row_single(a, (int)b, s);
+    row_single<false>(a, (int)b, s);
     return;
   }
   {
@@ -3729,10 +3760,28 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows(KernelArgs 
                per <= 32u * kThreads * kChainMaxQ) {
       topp_split(a, (int)b, sl, G, s);
     } else if (sl == 0) {
-      row_single(a, (int)b, s);
+      row_single<false>(a, (int)b, s);
     }
   }
   row_reset(a, b, s);
+}
+
+// One workgroup per row (launches that do not split rows): the whole
+// sampler of row blockIdx.x.
+extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows_single(KernelArgs args) {
+  (void)args;
+  const KernelArgs& a =
+      *reinterpret_cast<const KernelArgs*>(__builtin_amdgcn_kernarg_segment_ptr());
+  __shared__ Smem s;
+  LUMEN_TICK_INIT();
+  if (threadIdx.x == 0) s.finisher = 0u;
+  expf_table_init();
+  __syncthreads();
+  const uint32_t b = blockIdx.x;
+  if (b >= a.batch) return;
+  LUMEN_TICK_SLOT(b, 0u);
+  __syncthreads();
+  row_single<true>(a, (int)b, s);
 }
 
 // Penalty window counts from the device history ring, one workgroup per row
