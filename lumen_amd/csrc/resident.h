@@ -221,11 +221,17 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
 #ifdef LUMEN_TIMING
   LUMEN_TICK("rr_scan", LUMEN_TIMING_ROW);
 #endif
-  const double rel = 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
+  // the probe's margin is the drift of a probability sum from its estimate
+  // (the exact softmax sum divided out, from the slice's exact start):
+  // observed up to ~3e-5 of it; a sum estimated from the row start drifts
+  // by up to ~4e-9 of it per element
+  constexpr double kProbeRel = 1e-4;
+  const double rel = FIND ? kProbeRel : 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
   const uint32_t blo = est_binade(P * (1.0 - rel));
   const uint32_t bhi = est_binade((P + d) * (1.0 + rel));
   bool unc = live && blo != bhi;
-  if (FIND) unc = unc || (live && P * (1.0 - rel) <= (double)probe && (double)probe <= (P + d) * (1.0 + rel));
+  if (FIND)
+    unc = unc || (live && P * (1.0 - kProbeRel) <= (double)probe && (double)probe <= (P + d) * (1.0 + kProbeRel));
   const uint32_t bin = unc ? est_binade(P + 0.5 * d) : blo;
   float y0 = __uint_as_float(bin), y1 = __uint_as_float(bin | 1u);
 #pragma unroll
@@ -444,11 +450,20 @@ __device__ __forceinline__ void res_walk_at(uint32_t G, uint32_t nit, uint32_t r
           // a run: the crossing cannot lie in it
           if (FIND && r < __uint_as_float(cb + inc)) {
             good = 0;
+#ifdef LUMEN_FALLBACK_DEBUG
+            hit_k = k0 + q;
+            hit_j = 2u;
+#endif
             break;
           }
           cb += inc;
         } else {
           good = 0;
+#ifdef LUMEN_FALLBACK_DEBUG
+          hit_k = k0 + q;
+          hit_j = 1u;
+          before = cb;
+#endif
           break;
         }
         continue;
