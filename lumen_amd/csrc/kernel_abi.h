@@ -201,7 +201,7 @@ struct KernelArgs {
 // object whose stamp differs from its own: kernel arguments read with
 // another layout would be garbage pointers. kAbiVersion changes with any
 // change of meaning that keeps the sizes.
-constexpr uint32_t kAbiVersion = 4;
+constexpr uint32_t kAbiVersion = 6;
 constexpr uint32_t kAbiStamp =
     (kAbiVersion * 0x9E3779B1u) ^ ((uint32_t)sizeof(KernelArgs) * 0x85EBCA77u) ^
     ((uint32_t)sizeof(RowWs) * 0xC2B2AE3Du) ^ ((uint32_t)sizeof(RowParams) * 0x27D4EB2Fu) ^

@@ -82,14 +82,14 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
   }
   const uint32_t ip = pos & 0xffffu, rp = pos >> 16;
   if (unc) {
-    *reinterpret_cast<uint4*>(rec + 4u * ip) = make_uint4(bin, own.a0, own.a1, FIND ? rp | (t << 16) : rp);
-    uint4* raw = reinterpret_cast<uint4*>(rec + kRsRawOff + kResK * rp);
+    gst(reinterpret_cast<u32x4*>(rec + 4u * ip), u32x4{bin, own.a0, own.a1, FIND ? rp | (t << 16) : rp});
+    u32x4* raw = reinterpret_cast<u32x4*>(rec + kRsRawOff + kResK * rp);
 #pragma unroll
     for (int m = 0; m < (int)kResK / 4; ++m)
-      raw[m] = make_uint4(__float_as_uint(e[4 * m]), __float_as_uint(e[4 * m + 1]),
-                          __float_as_uint(e[4 * m + 2]), __float_as_uint(e[4 * m + 3]));
+      gst(raw + m, u32x4{__float_as_uint(e[4 * m]), __float_as_uint(e[4 * m + 1]),
+                         __float_as_uint(e[4 * m + 2]), __float_as_uint(e[4 * m + 3])});
   } else if (last) {
-    *reinterpret_cast<uint4*>(rec + 4u * ip) = make_uint4(bin, inc.m.a0, inc.m.a1, kNoRaw);
+    gst(reinterpret_cast<u32x4*>(rec + 4u * ip), u32x4{bin, inc.m.a0, inc.m.a1, kNoRaw});
   }
   return rc;
 }
@@ -99,10 +99,10 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
 __device__ __forceinline__ void row_load32(const Row& row, uint32_t i0, float (&v)[kResK]) {
   if (i0 + kResK <= row.V && row.vec) {
     if (row.f) {
-      const float4* p = reinterpret_cast<const float4*>(row.f + i0);
-      float4 q[kResK / 4];
+      const f32x4* p = reinterpret_cast<const f32x4*>(row.f + i0);
+      f32x4 q[kResK / 4];
 #pragma unroll
-      for (int m = 0; m < (int)kResK / 4; ++m) q[m] = p[m];
+      for (int m = 0; m < (int)kResK / 4; ++m) q[m] = gld(p + m);
 #pragma unroll
       for (int m = 0; m < (int)kResK / 4; ++m) {
         v[4 * m] = q[m].x;
@@ -111,10 +111,10 @@ __device__ __forceinline__ void row_load32(const Row& row, uint32_t i0, float (&
         v[4 * m + 3] = q[m].w;
       }
     } else {
-      const ushort4* p = reinterpret_cast<const ushort4*>(row.h + i0);
-      ushort4 q[kResK / 4];
+      const u16x4* p = reinterpret_cast<const u16x4*>(row.h + i0);
+      u16x4 q[kResK / 4];
 #pragma unroll
-      for (int m = 0; m < (int)kResK / 4; ++m) q[m] = p[m];
+      for (int m = 0; m < (int)kResK / 4; ++m) q[m] = gld(p + m);
 #pragma unroll
       for (int m = 0; m < (int)kResK / 4; ++m) {
         v[4 * m] = __uint_as_float((uint32_t)q[m].x << 16);
@@ -169,7 +169,7 @@ __device__ __forceinline__ bool rec_gather_small(const KernelArgs& a, int b, uin
       while (i + 1u < G && rb[i + 1] <= r) ++i;
       src = rs_rec(a, b, i) + kRsRawOff + kResK * (r - rb[i]) + (f - rawbase) % kResK;
     }
-    words[f] = *src;
+    words[f] = gld(src);
   }
   __syncthreads();
   *nit_out = nit;

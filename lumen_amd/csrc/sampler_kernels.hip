@@ -146,22 +146,41 @@ __device__ __forceinline__ float rmax(float a, float b) {
   return a > b ? a : b;
 }
 
+// Loads and stores through global-memory pointers. The row and workspace
+// pointers reach the noinline per-row functions as generic pointers, for
+// which the compiler emits flat instructions: those count against the LDS
+// wait counter too, so every LDS wait also drains the outstanding row loads.
+// The casts give global_load / global_store.
+// (Scalars and clang vector types only: a HIP_vector_type goes through its
+// copy constructor, whose generic reference loses the address space.)
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <class T>
+__device__ __forceinline__ T gld(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+template <class T>
+__device__ __forceinline__ void gst(T* p, T v) {
+  *(__attribute__((address_space(1))) T*)p = v;
+}
+
 struct Row {
   const float* f;
   const uint16_t* h;
   uint32_t V;
   bool vec;
   __device__ __forceinline__ float at(uint32_t i) const {
-    return f ? f[i] : __uint_as_float((uint32_t)h[i] << 16);
+    return f ? gld(f + i) : __uint_as_float((uint32_t)gld(h + i) << 16);
   }
   // elements i..i+3 (i % 4 == 0); out-of-range lanes are left untouched
   __device__ __forceinline__ void load4(uint32_t i, float (&v)[4]) const {
     if (vec && i + 3 < V) {
       if (f) {
-        float4 q = *reinterpret_cast<const float4*>(f + i);
+        const f32x4 q = gld(reinterpret_cast<const f32x4*>(f + i));
         v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
       } else {
-        ushort4 q = *reinterpret_cast<const ushort4*>(h + i);
+        const u16x4 q = gld(reinterpret_cast<const u16x4*>(h + i));
         v[0] = __uint_as_float((uint32_t)q.x << 16);
         v[1] = __uint_as_float((uint32_t)q.y << 16);
         v[2] = __uint_as_float((uint32_t)q.z << 16);
@@ -1791,8 +1810,11 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
   __syncthreads();
   const bool found = s.misc_u[0] != 0u;
   const uint32_t rank = s.misc_u[1];
-  pk_lo = s.misc_u[2];
-  pk_hi = s.misc_u[3];
+  // the group bounds in registers: the loops below must not re-read them
+  // through the output references (their stores may alias LDS atomics)
+  const uint32_t glo = s.misc_u[2], ghi = s.misc_u[3];
+  pk_lo = glo;
+  pk_hi = ghi;
   tr.topp_cum = s.red_f[0];
   __syncthreads();
   LUMEN_TICK("bv_walk", LUMEN_TIMING_ROW);
@@ -1803,7 +1825,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
   tr.topp_kept = rank;
   // tokens with a larger p: the counts of the values above pk_hi
   uint32_t gt = 0;
-  for (uint32_t pk = pk_hi + 1u + t; pk <= 0xffffu; pk += kThreads) gt += vcount(cw, pk);
+  for (uint32_t pk = ghi + 1u + t; pk <= 0xffffu; pk += kThreads) gt += vcount(cw, pk);
   gt = block_sum_u32(gt, s);
   LUMEN_TICK("bv_gt", LUMEN_TIMING_ROW);
   // the kept set ends at the (rank - gt)-th id, in id order, of the tokens
@@ -1816,7 +1838,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
   __syncthreads();
   row_foreach(row, [&](uint32_t i, float v) {
     const uint32_t pk = tkey(vf(i, v)) >> 16;
-    if (pk >= pk_lo && pk <= pk_hi) atomicAdd(&s.H[2047u - (i >> sh)], 1u);
+    if (pk >= glo && pk <= ghi) atomicAdd(&s.H[2047u - (i >> sh)], 1u);
   });
   __syncthreads();  // every wave's counts are in before the search reads them
   tr.passes++;
@@ -1831,7 +1853,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
   __syncthreads();
   range_foreach(row, lo, hi, [&](uint32_t i, float v) {
     const uint32_t pk = tkey(vf(i, v)) >> 16;
-    if (pk >= pk_lo && pk <= pk_hi) atomicOr(&bits[(i - lo) >> 5], 1u << ((i - lo) & 31u));
+    if (pk >= glo && pk <= ghi) atomicOr(&bits[(i - lo) >> 5], 1u << ((i - lo) & 31u));
   });
   __syncthreads();
   if (t == 0) {
@@ -1924,7 +1946,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   const uint32_t h0 = a.hist_off[b], h1 = hist_hi(a, b);
   if ((P.flags & kPen) && h1 > h0) {
     float* dst = a.pen_scratch + (uint64_t)b * a.pen_stride;
-    row_foreach(row, [&](uint32_t i, float v) { dst[i] = v; });
+    row_foreach(row, [&](uint32_t i, float v) { gst(dst + i, v); });
     __syncthreads();
     for (uint32_t j = h0 + t; j < h1; j += kThreads) {
       uint32_t id = a.hist_ids[j];
@@ -1938,7 +1960,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   }
   if (a.pen_out) {
     float* po = a.pen_out + (uint64_t)b * V;
-    row_foreach(row, [&](uint32_t i, float v) { po[i] = v; });
+    row_foreach(row, [&](uint32_t i, float v) { gst(po + i, v); });
   }
 
   // ---- greedy (sampling.rs:468-476) ----
@@ -2105,18 +2127,17 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       // softmax sum at T = 1 and, for the window path, a key histogram of the
       // positive-probability tokens (bf16 rows walk their value counts
       // instead, and build it only if that walk cannot run)
+      auto e1f = [&](uint32_t, float v) -> float { return expf_glibc(__fsub_rn(v1f(v), m1)); };
       bool rec_ok = false;
       EcssResult e{0.f, 0, -1, 0.f};
-      if (V2 && bf)
-        e = row_rec_sum<false>(a, b, row, [&](uint32_t, float v) { return expf_glibc(__fsub_rn(v1f(v), m1)); },
-                               0.f, s, rec_ok);
+      if (V2 && bf) e = row_rec_sum<false>(a, b, row, e1f, 0.f, s, rec_ok);
       if (!rec_ok) {
         clear_hist(s.H0, 2048);
         __syncthreads();
         e = row_ecss(
             row,
             [&](uint32_t i, float v) {
-              float x = expf_glibc(__fsub_rn(v1f(v), m1));
+              float x = e1f(i, v);
               if (!bf && x > 0.f) atomicAdd(&s.H0[tkey(v) >> 21], 1u);
               return x;
             },
@@ -2384,16 +2405,22 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   }
 
   // ---- large path: min-p, temperature, softmax, draw over the whole row ----
-  auto v2f = [&](uint32_t i, float v) -> float {
-    float x = v1f(v);
-    if (pmode == 1) {
-      if (i > plim) x = kNegInf;
-    } else if (pmode == 2) {
-      float p = __fdiv_rn(expf_glibc(__fsub_rn(x, m1)), S1);
-      if (!(p > pstar || (p == pstar && i <= istar))) x = kNegInf;
-    } else if (pmode == 3) {
+  // The masks' state as values: some of it went out by reference, and the
+  // per-element passes below must not re-read it from memory.
+  const bool c_kmask = kmask;
+  const uint32_t c_kcut = kcut, c_plim = plim, c_istar = istar, c_pk_lo = pk_lo, c_pk_hi = pk_hi;
+  const int c_pmode = pmode;
+  const float c_m1 = m1, c_S1 = S1, c_pstar = pstar;
+  auto v2f = [=](uint32_t i, float v) -> float {
+    float x = (c_kmask && tkey(v) < c_kcut) ? kNegInf : v;
+    if (c_pmode == 1) {
+      if (i > c_plim) x = kNegInf;
+    } else if (c_pmode == 2) {
+      float p = __fdiv_rn(expf_glibc(__fsub_rn(x, c_m1)), c_S1);
+      if (!(p > c_pstar || (p == c_pstar && i <= c_istar))) x = kNegInf;
+    } else if (c_pmode == 3) {
       const uint32_t pk = tkey(x) >> 16;
-      if (!(pk > pk_hi || (pk >= pk_lo && i <= istar))) x = kNegInf;
+      if (!(pk > c_pk_hi || (pk >= c_pk_lo && i <= c_istar))) x = kNegInf;
     }
     return x;
   };
@@ -2410,10 +2437,12 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       bound = __fadd_rn(m, P.log_min_p);
     }
   }
-  auto wf = [&](uint32_t i, float v) -> float {
+  const float c_bound = bound, c_inv_temp = P.inv_temp;
+  const bool c_mmask = mmask;
+  auto wf = [=](uint32_t i, float v) -> float {
     float x = v2f(i, v);
-    if (mmask && x < bound) x = kNegInf;
-    return __fmul_rn(x, P.inv_temp);
+    if (c_mmask && x < c_bound) x = kNegInf;
+    return __fmul_rn(x, c_inv_temp);
   };
   float m3 = kNegInf;
   uint32_t nan3 = 0;
@@ -2449,32 +2478,114 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
     tr.cdf_before = tr.cdf_at = __uint_as_float(0x7fc00000u);
     tok = V - 1;
   } else {
+    // bf16 rows of lumen_sample_rows_single: a summand is a function of
+    // the element's bit pattern and of whether its index lies past the
+    // masks' index split (pmode 1: plim, 2 and 3: istar), so the sums read
+    // it from two LDS tables (lists A and B: index <= split, index > split)
+    // over a window of 64 binades of |value| per sign. Live summands have
+    // |w| <= W = max(|m3|, |m3 - 128|) (below m3 - 128, exp gives 0), so
+    // every pattern above the window (|v| >= 2^(emax - 126) > 2 W / inv_temp)
+    // is zero; patterns below it (|v| < 2^(emax - 190)) take the direct
+    // computation.
+    const bool ftab = V2 && row.h != nullptr;
+    float* const TA = reinterpret_cast<float*>(s.A);
+    float* const TB = reinterpret_cast<float*>(s.Bk);
+    static_assert(sizeof(s.A) == 16384 * sizeof(float) && sizeof(s.Bk) == sizeof(s.A),
+                  "two tables of 2 x 64 x 128 entries");
+    uint32_t wlo = 0, whi = 0;
+    const uint32_t isplit = c_pmode == 1 ? c_plim : (c_pmode >= 2 ? c_istar : 0xffffffffu);
+    if (ftab) {
+      const float W = fmaxf(fabsf(m3), fabsf(__fsub_rn(m3, 128.f)));
+      const float vm = __fdiv_rn(W, c_inv_temp);
+      uint32_t emax = ((__float_as_uint(vm) >> 23) & 0xffu) + 1u;
+      emax = emax > 254u ? 254u : (emax < 63u ? 63u : emax);
+      wlo = (emax - 63u) << 7;
+      whi = (emax + 1u) << 7;
+      // value counts still in lists A and B (the by-value walk ran on exact
+      // counts): patterns the row does not hold get no exp
+      const bool counted = c_pmode == 3;
+      uint32_t present = 0xffffu;
+      if (counted) {
+        const uint32_t* cw = bv_counts(s);
+        present = 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 16u; ++k) {
+          const uint32_t j = threadIdx.x + k * kThreads;
+          const uint32_t pat = ((j >> 13) << 15) | (wlo + (j & 8191u));
+          if (vcount(cw, tkey(__uint_as_float(pat << 16)) >> 16) != 0u) present |= 1u << k;
+        }
+        __syncthreads();
+      }
+#pragma unroll 1
+      for (uint32_t k = 0; k < 16u; ++k) {
+        const uint32_t j = threadIdx.x + k * kThreads;
+        float ea = 0.f, eb = 0.f;
+        if ((present >> k) & 1u) {
+          const float v = __uint_as_float((((j >> 13) << 15) | (wlo + (j & 8191u))) << 16);
+          float x = (c_kmask && tkey(v) < c_kcut) ? kNegInf : v;
+          bool ka = true, kb = true;  // kept at an index <= / > the split
+          if (c_pmode == 1) {
+            kb = false;
+          } else if (c_pmode == 2) {
+            const float pp = __fdiv_rn(expf_glibc(__fsub_rn(x, c_m1)), c_S1);
+            ka = pp >= c_pstar;
+            kb = pp > c_pstar;
+          } else if (c_pmode == 3) {
+            const uint32_t pk = tkey(x) >> 16;
+            ka = pk >= c_pk_lo;
+            kb = pk > c_pk_hi;
+          }
+          if (c_mmask && x < c_bound) x = kNegInf;
+          const float w = __fmul_rn(x, c_inv_temp);
+          const float e = w == kNegInf ? 0.f : expf_glibc(__fsub_rn(w, m3));
+          ea = ka ? e : 0.f;
+          eb = kb ? e : 0.f;
+        }
+        TA[j] = ea;
+        TB[j] = eb;
+      }
+      __syncthreads();
+    }
+    auto e3f = [&](uint32_t i, float v) -> float {
+      if (ftab) {
+        const uint32_t p = __float_as_uint(v) >> 16, q = (p & 0x7fffu) - wlo;
+        if (q < 8192u) return (i <= isplit ? TA : TB)[q + ((p >> 15) << 13)];
+        if ((p & 0x7fffu) >= whi) return 0.f;
+      }
+      const float w = wf(i, v);
+      return w == kNegInf ? 0.f : expf_glibc(__fsub_rn(w, m3));
+    };
     bool rec_ok = false;
     EcssResult S{0.f, 0, -1, 0.f};
-    if (V2)
-      S = row_rec_sum<false>(
-          a, b, row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, 0.f, s,
-          rec_ok);
-    if (!rec_ok)
-      S = row_ecss(
-          row, [&](uint32_t i, float v) { return expf_glibc(__fsub_rn(wf(i, v), m3)); }, kEcssSum,
-          0.f, s);
+    if (V2) S = row_rec_sum<false>(a, b, row, e3f, 0.f, s, rec_ok);
+    if (!rec_ok) S = row_ecss(row, e3f, kEcssSum, 0.f, s);
     tr.passes++;
     LUMEN_TICK("rs_S3", b);
     const float S3 = S.c;
     tr.final_sum = S3;
+    if (ftab) {
+      // each thread divides the entries it wrote
+#pragma unroll 1
+      for (uint32_t k = 0; k < 16u; ++k) {
+        const uint32_t j = threadIdx.x + k * kThreads;
+        TA[j] = __fdiv_rn(TA[j], S3);
+        TB[j] = __fdiv_rn(TB[j], S3);
+      }
+      __syncthreads();
+    }
+    auto p3f = [&](uint32_t i, float v) -> float {
+      if (ftab) {
+        const uint32_t p = __float_as_uint(v) >> 16, q = (p & 0x7fffu) - wlo;
+        if (q < 8192u) return (i <= isplit ? TA : TB)[q + ((p >> 15) << 13)];
+        if ((p & 0x7fffu) >= whi) return 0.f;
+      }
+      const float w = wf(i, v);
+      return __fdiv_rn(w == kNegInf ? 0.f : expf_glibc(__fsub_rn(w, m3)), S3);
+    };
     EcssResult e{0.f, 0, -1, 0.f};
     rec_ok = false;
-    if (V2)
-      e = row_rec_sum<true>(
-          a, b, row,
-          [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
-          rdraw, s, rec_ok);
-    if (!rec_ok)
-      e = row_ecss(
-          row,
-          [&](uint32_t i, float v) { return __fdiv_rn(expf_glibc(__fsub_rn(wf(i, v), m3)), S3); },
-          kEcssFindGt, rdraw, s);
+    if (V2) e = row_rec_sum<true>(a, b, row, p3f, rdraw, s, rec_ok);
+    if (!rec_ok) e = row_ecss(row, p3f, kEcssFindGt, rdraw, s);
     tr.passes++;
     LUMEN_TICK("rs_cdf", b);
     tr.cdf_before = e.found ? e.before : e.c;
