@@ -28,20 +28,41 @@ __device__ __forceinline__ uint32_t* rs_rec(const KernelArgs& a, int b, uint32_t
 
 // res_record for summands held in registers, into an area of kRsBlockWords
 // words (at most kRsItemCap items, kRsRawCap raws); also returns the
-// block's f64 total (the estimate of the next block's start).
+// block's f64 total (the estimate of the next block's start). Three
+// barriers: the f64 prefix, the neighbours' class codes at wave edges, and
+// the wave totals of the segmented run scan and of the item / raw counts
+// (each wave combines the totals of the waves before it itself). Its LDS
+// scratch (s.H0[0 .. 191]) is rewritten only after the next two barriers,
+// so consecutive calls need none in between.
 template <bool FIND>
 __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], double p_slice,
                                                     uint32_t pos0, uint32_t nthr, uint32_t* rec,
                                                     Smem& s, float probe, double* tot_out) {
-  const uint32_t t = threadIdx.x;
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
   const bool live = t < nthr;
-  double d = 0.0;
+  // the thread's total, pairwise in f32: relative error below 3e-7, far
+  // inside the margins below
+  float q8[kResK / 8];
 #pragma unroll
-  for (int m = 0; m < (int)kResK / 4; ++m)
-    d += ((double)e[4 * m] + (double)e[4 * m + 1]) + ((double)e[4 * m + 2] + (double)e[4 * m + 3]);
-  double tot;
-  const double P = p_slice + block_excl_scan_f64(d, s, &tot);
+  for (int m = 0; m < (int)kResK / 8; ++m)
+    q8[m] = ((e[8 * m] + e[8 * m + 1]) + (e[8 * m + 2] + e[8 * m + 3])) +
+            ((e[8 * m + 4] + e[8 * m + 5]) + (e[8 * m + 6] + e[8 * m + 7]));
+  const double d = (double)((q8[0] + q8[1]) + (q8[2] + q8[3]));
+  // 1. f64 prefix of the thread totals: the estimated running sum at the
+  // thread's start
+  double* wt = reinterpret_cast<double*>(s.H0);  // [kWaves]
+  const double dinc = wave_scan_incl(d, 0.0, [](double l, double r) { return l + r; });
+  if (lane == 63u) wt[w] = dinc;
+  __syncthreads();
+  double pre = 0.0, tot = 0.0;
+#pragma unroll
+  for (uint32_t i = 0; i < (uint32_t)kWaves; ++i) {
+    const double x = wt[i];
+    if (i < w) pre += x;
+    tot += x;
+  }
   *tot_out = tot;
+  const double P = p_slice + pre + (dinc - d);
   const double rel = 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
   const uint32_t blo = est_binade(P * (1.0 - rel));
   const uint32_t bhi = est_binade((P + d) * (1.0 + rel));
@@ -60,21 +81,49 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
   }
   const uint32_t n0 = __float_as_uint(y0) - bin, n1 = __float_as_uint(y1) - (bin | 1u);
   const PMap own{n0 > kSat ? kSat : n0, n1 > kSat ? kSat : n1};
+  // 2. class codes of the neighbours (runs are maximal spans of certain
+  // threads in one binade)
   constexpr uint32_t kUnc = 1u, kDead = 2u;
-  uint32_t* cls = s.H0;
   const uint32_t code = !live ? kDead : unc ? kUnc : bin;
-  cls[t] = code;
+  uint32_t* bc = s.H0 + 64;  // [kWaves][2]: first and last code of each wave
+  if (lane == 0u) bc[2u * w] = code;
+  if (lane == 63u) bc[2u * w + 1u] = code;
   __syncthreads();
-  const uint32_t prv = t > 0 ? cls[t - 1] : kDead;
-  const uint32_t nxt = t + 1 < (uint32_t)kThreads ? cls[t + 1] : kDead;
+  uint32_t prv = wave_shr1(code, kDead);
+  if (lane == 0u) prv = w > 0u ? bc[2u * w - 1u] : kDead;
+  uint32_t nxt = (uint32_t)__shfl_down((int)code, 1);
+  if (lane == 63u) nxt = w + 1u < (uint32_t)kWaves ? bc[2u * w + 2u] : kDead;
   const bool head = live && (unc || prv != code);
   const bool last = live && !unc && nxt != code;
-  SegVal prev;
-  const SegVal inc = seg_scan_incl(SegVal{head ? 1u : 0u, (live && !unc) ? own : PMap{0u, 0u}},
-                                   s.ecss, s.est, &prev);
   const uint32_t packed = ((unc || last) ? 1u : 0u) | ((unc ? 1u : 0u) << 16);
-  uint32_t ptot;
-  const uint32_t pos = block_excl_scan_u32(packed, s, &ptot);
+  // 3. the segmented scan of the run maps and the scan of the item / raw
+  // counts, wave by wave, then across the waves
+  const SegVal id{0u, PMap{0u, 0u}};
+  const SegVal sinc = wave_scan_incl(SegVal{head ? 1u : 0u, (live && !unc) ? own : PMap{0u, 0u}}, id,
+                                     seg_combine);
+  const uint32_t pinc = wave_scan_incl(packed, 0u, op_add_u32);
+  uint32_t* st = s.H0 + 128;  // [kWaves][4]: head, a0, a1, count total
+  if (lane == 63u) {
+    st[4u * w] = sinc.head;
+    st[4u * w + 1u] = sinc.m.a0;
+    st[4u * w + 2u] = sinc.m.a1;
+    st[4u * w + 3u] = pinc;
+  }
+  __syncthreads();
+  SegVal spre = id;
+  uint32_t ppre = 0, ptot = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < (uint32_t)kWaves; ++i) {
+    const SegVal x{st[4u * i], PMap{st[4u * i + 1u], st[4u * i + 2u]}};
+    const uint32_t c = st[4u * i + 3u];
+    if (i < w) {
+      spre = seg_combine(spre, x);
+      ppre += c;
+    }
+    ptot += c;
+  }
+  const SegVal inc = seg_combine(spre, sinc);
+  const uint32_t pos = ppre + pinc - packed;
   RecCount rc{ptot & 0xffffu, ptot >> 16, true};
   if (rc.items > kRsItemCap || rc.raws > kRsRawCap) {
     rc.ok = false;
@@ -205,10 +254,12 @@ __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, co
       const uint32_t i = lo + t * kResK + (uint32_t)k;
       e[k] = i < V ? xf(i, e[k]) : 0.f;
     }
+    LUMEN_TICK("rr_x", b);
     double tot;
     const RecCount rc = res_record_regs<FIND>(e, P, lo, (n + kResK - 1u) / kResK, rs_rec(a, b, blk),
                                               s, probe, &tot);
     P += tot;
+    LUMEN_TICK("rr_rec", b);
     if (t == 0) {
       nrec[blk] = rc.items;
       nraw[blk] = rc.raws;
@@ -225,8 +276,10 @@ __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, co
   __syncthreads();
   uint32_t nit = 0, rawbase = 0;
   if (!fit || !rec_gather_small(a, b, nb, nrec, nraw, s, &nit, &rawbase)) return r;
+  LUMEN_TICK("rr_gather", b);
   if (t < 64u) res_walk_at<FIND>(nb, nit, rawbase, probe, s.H, s);
   __syncthreads();
+  LUMEN_TICK("rr_walk", b);
   const bool found = s.misc_u[1] != 0u;
   // a search cut short must have found its hit
   ok = s.misc_u[0] != 0u && (found || nb == nblk);

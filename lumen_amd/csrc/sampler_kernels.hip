@@ -199,7 +199,36 @@ struct Row {
 template <class F>
 __device__ __forceinline__ void row_foreach(const Row& r, F&& f) {
   const uint32_t V = r.V;
-  for (uint32_t g0 = threadIdx.x; g0 * 4u < V; g0 += 4u * kThreads) {
+  uint32_t g0 = threadIdx.x;
+  // whole groups of 4 x 4 elements on aligned rows: no per-element checks
+  if (r.vec) {
+    for (; (g0 + 3u * kThreads) * 4u + 3u < V; g0 += 4u * kThreads) {
+      float v[4][4];
+      if (r.f) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f32x4 q = gld(reinterpret_cast<const f32x4*>(r.f) + g0 + u * kThreads);
+          v[u][0] = q.x; v[u][1] = q.y; v[u][2] = q.z; v[u][3] = q.w;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const u16x4 q = gld(reinterpret_cast<const u16x4*>(r.h) + g0 + u * kThreads);
+          v[u][0] = __uint_as_float((uint32_t)q.x << 16);
+          v[u][1] = __uint_as_float((uint32_t)q.y << 16);
+          v[u][2] = __uint_as_float((uint32_t)q.z << 16);
+          v[u][3] = __uint_as_float((uint32_t)q.w << 16);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t i = (g0 + u * kThreads) * 4u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f(i + j, v[u][j]);
+      }
+    }
+  }
+  for (; g0 * 4u < V; g0 += 4u * kThreads) {
     float v[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -1697,27 +1726,37 @@ __device__ __forceinline__ void bv_count(float x, Smem& s) {
   atomicAdd(&bv_counts(s)[pk >> 1], 1u << ((pk & 1u) << 4));
 }
 
-// Per block of 256 values, the sum of the u16 counts into s.H[0 .. 255];
+// Per block of 256 values, the sum of the u16 counts into s.H[0 .. 255] and
+// the number of distinct values present into s.H[256 .. 511];
 // returns (uniformly) whether the counts are exact: a u16 count that
 // overflowed lost 65535 or 65536 (its carry goes to the neighbour or out of
 // the word), so the counts are exact iff they add up to the n elements
 // counted.
 __device__ __forceinline__ bool bv_blocks(uint32_t n, Smem& s) {
-  const uint32_t t = threadIdx.x;
+  const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
   const uint32_t* cw = bv_counts(s);
-  uint32_t part = 0;  // values 64t .. 64t+63 (32 words)
-#pragma unroll 8
-  for (uint32_t i = 0; i < 32u; ++i) {
-    const uint32_t w = cw[32u * t + i];
-    part += (w & 0xffffu) + (w >> 16);
+  // wave w sums blocks 16w .. 16w+15 (128 words each), its lanes reading
+  // consecutive words (no bank conflicts)
+  uint32_t part = 0;
+#pragma unroll 2
+  for (uint32_t j = 0; j < 16u; ++j) {
+    const uint32_t w0 = cw[(16u * w + j) * 128u + lane], w1 = cw[(16u * w + j) * 128u + 64u + lane];
+    const uint32_t c = (w0 & 0xffffu) + (w0 >> 16) + (w1 & 0xffffu) + (w1 >> 16);
+    const uint32_t d = ((w0 & 0xffffu) != 0u ? 1u : 0u) + ((w0 >> 16) != 0u ? 1u : 0u) +
+                       ((w1 & 0xffffu) != 0u ? 1u : 0u) + ((w1 >> 16) != 0u ? 1u : 0u);
+    const uint32_t cs = wave_reduce(c, 0u, op_add_u32), ds = wave_reduce(d, 0u, op_add_u32);
+    if (lane == 0) {
+      s.H[16u * w + j] = cs;
+      s.H[256u + 16u * w + j] = ds;
+    }
+    part += c;
   }
-  // 4 consecutive threads (lanes) hold one block of 256 values
-  uint32_t blk = part + __shfl_xor(part, 1);
-  blk += __shfl_xor(blk, 2);
-  if ((t & 3u) == 0u) s.H[t >> 2] = blk;
   const uint32_t tot = block_sum_u32(part, s);
   return tot == n;
 }
+
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, Smem& s, uint32_t* total);
+__device__ __forceinline__ double block_excl_scan_f64(double v, Smem& s, double* total);
 
 // The value with key upper half pk: a negative value's key carries ones in
 // its low 16 bits.
@@ -1749,31 +1788,136 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
   if (V > (1u << 22) || !bv_blocks(V, s)) return -1;
   __syncthreads();
   auto pof = [&](uint32_t pk) { return __fdiv_rn(expf_glibc(__fsub_rn(bv_value(pk), m1)), S1); };
-  if (t < 64u) {
-    const uint32_t lane = t;
-    float c = 0.f;
-    uint32_t rank = 0, pks = 0;
-    ValHit h{false, 0u, 0u, 0.f};
-    float ph = 0.f;
-    for (int blk = 255; blk >= 0 && !h.found; --blk) {
-      if (s.H[blk] == 0u) continue;
-      LUMEN_TICK("bv_blk", LUMEN_TIMING_ROW);
-      for (int sub = 3; sub >= 0; --sub) {
-        const uint32_t pk = (uint32_t)blk * 256u + (uint32_t)sub * 64u + (63u - lane);
-        const uint32_t cnt = vcount(cw, pk);
-        if (__ballot(cnt != 0u) == 0ull) continue;
-        const float p = cnt ? pof(pk) : 0.f;
-        h = wave_values(c, p, cnt, top_p);
-        if (h.found) {
-          rank += wave_reduce(lane < h.lane ? cnt : 0u, 0u, op_add_u32) + h.j + 1u;
-          ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), (int)h.lane));
-          pks = (uint32_t)__builtin_amdgcn_readlane((int)pk, (int)h.lane);
-          break;
-        }
-        rank += wave_reduce(cnt, 0u, op_add_u32);
+  // The walk in rounds of at most 1024 present values (descending), every
+  // wave taking 64 of them: the parity map of its 64 values' adds for the
+  // binade its start is estimated in (f64 prefix of count x p), then wave 0
+  // composes the waves in order from the exact running sum, taking a wave's
+  // map whenever the exact sum starts in that binade and ends in it below
+  // top_p, and replaying the wave value by value (wave_values) otherwise.
+  uint32_t* const list = s.H + 512;               // [1024] (pk << 16) | count
+  float* const pl = reinterpret_cast<float*>(s.H + 1536);  // [1024] p
+  uint32_t* const wv = s.H + 2560;                // [16][4] binade, a0, a1, count sum
+  const uint32_t lane = t & 63u, w = t >> 6;
+  float c = 0.f;
+  uint32_t wrank = 0, pks = 0;
+  float ph = 0.f;
+  bool hit = false;
+  int bh = 255;  // next block (of 256 values) to take, descending
+  while (bh >= 0 && !hit) {
+    // plan: whole blocks while their distinct values fit in 1024
+    if (t < 64u) {
+      uint32_t take = 0, tot = 0;
+      for (int base = bh; base >= 0; base -= 64) {
+        const int blk = base - (int)lane;
+        const uint32_t d = blk >= 0 ? s.H[256 + blk] : 0u;
+        const uint32_t inc = wave_scan_incl(d, 0u, op_add_u32);
+        const unsigned long long fit = __ballot(blk >= 0 && tot + inc <= 1024u);
+        // blocks are taken while the running total fits (a prefix of lanes)
+        const uint32_t nfit = fit == ~0ull ? 64u : (uint32_t)__ffsll((long long)~fit) - 1u;
+        take += nfit;
+        if (nfit > 0u) tot += (uint32_t)__builtin_amdgcn_readlane((int)inc, (int)nfit - 1);
+        if (nfit < 64u) break;
+      }
+      if (take == 0u) take = 1u;  // a block never holds more than 256 values
+      if (lane == 0) {
+        s.misc_i[0] = bh - (int)take;  // the round covers blocks (bh - take, bh]
+        s.misc_u[0] = tot;
       }
     }
-    LUMEN_TICK("bv_cross", LUMEN_TIMING_ROW);
+    __syncthreads();
+    const int bl = s.misc_i[0];
+    __syncthreads();
+    LUMEN_TICK("bv_plan", LUMEN_TIMING_ROW);
+    // compaction of the present values of blocks (bl, bh], descending: wave
+    // w takes keys khi - 1 - [w * wspan, (w + 1) * wspan), 64 consecutive
+    // keys per step (one per lane), and places them by ballot
+    const uint32_t khi = (uint32_t)(bh + 1) * 256u, klo = (uint32_t)(bl + 1) * 256u;
+    const uint32_t span = khi - klo, wspan = (span + 64u * kWaves - 1u) / (64u * kWaves) * 64u;
+    uint32_t mine = 0;
+    for (uint32_t q = 0; q < wspan; q += 64u) {
+      const uint32_t off = w * wspan + q + lane;
+      mine += (uint32_t)__popcll(__ballot(off < span && vcount(cw, khi - 1u - off) != 0u));
+    }
+    uint32_t n;
+    uint32_t at = block_excl_scan_u32(lane == 0 ? mine : 0u, s, &n);
+    at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+    for (uint32_t q = 0; q < wspan && mine; q += 64u) {
+      const uint32_t off = w * wspan + q + lane;
+      const uint32_t pk = khi - 1u - off;
+      const uint32_t cnt = off < span ? vcount(cw, pk) : 0u;
+      const unsigned long long bm = __ballot(cnt != 0u);
+      const uint32_t pos = at + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull));
+      if (cnt && pos < 1024u) list[pos] = (pk << 16) | cnt;
+      at += (uint32_t)__popcll(bm);
+    }
+    __syncthreads();
+    if (n > 1024u) n = 1024u;  // cannot happen: the plan bounds the round
+    LUMEN_TICK("bv_list", LUMEN_TIMING_ROW);
+    // every wave: its values' p, the f64 estimate of its start, its map
+    const uint32_t e = t < n ? list[t] : 0u;
+    const uint32_t cnt = e & 0xffffu;
+    const float p = cnt ? pof(e >> 16) : 0.f;
+    pl[t] = p;
+    double tot_d;
+    const double pre = block_excl_scan_f64((double)cnt * (double)p, s, &tot_d);
+    const double st = (double)c + __shfl(pre, 0);
+    const uint32_t E = est_binade(st) >> 23;
+    const PMap m = rep_map(p, cnt, E);
+    const PMap mt = wave_read(wave_scan_incl(m, PMap{0u, 0u}, pm_combine), 63);
+    const uint32_t cs = wave_reduce(cnt, 0u, op_add_u32);
+    if (lane == 0) {
+      wv[4 * w] = E;
+      wv[4 * w + 1] = mt.a0;
+      wv[4 * w + 2] = mt.a1;
+      wv[4 * w + 3] = cs;
+    }
+    __syncthreads();
+    LUMEN_TICK("bv_maps", LUMEN_TIMING_ROW);
+    if (t < 64u) {
+      for (uint32_t ww = 0; ww < (n + 63u) / 64u; ++ww) {
+        const uint32_t cb = __float_as_uint(c);
+        const uint32_t ub = (cb & 0xff800000u) + 0x00800000u;
+        const uint32_t wE = wv[4 * ww], a0 = wv[4 * ww + 1], a1 = wv[4 * ww + 2], wc = wv[4 * ww + 3];
+        const uint32_t st2 = (cb & 1u) ? a1 : a0;
+        if ((cb >> 23) == wE && st2 < kSat && st2 < ub - cb && __uint_as_float(cb + st2) < top_p) {
+          c = __uint_as_float(cb + st2);
+          wrank += wc;
+          continue;
+        }
+        LUMEN_TICK("bv_fb", LUMEN_TIMING_ROW);
+        const uint32_t k = 64u * ww + lane;
+        const uint32_t ck = k < n ? (list[k] & 0xffffu) : 0u;
+        const float pk_p = k < n ? pl[k] : 0.f;
+        const ValHit h = wave_values(c, pk_p, ck, top_p);
+        if (h.found) {
+          wrank += wave_reduce(lane < h.lane ? ck : 0u, 0u, op_add_u32) + h.j + 1u;
+          ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pk_p), (int)h.lane));
+          pks = (uint32_t)__builtin_amdgcn_readlane((int)(list[64u * ww + h.lane] >> 16), 0);
+          hit = true;
+          break;
+        }
+        wrank += wc;
+      }
+      if (lane == 0) {
+        s.misc_u[1] = hit ? 1u : 0u;
+        s.red_f[1] = c;
+        s.misc_u[2] = wrank;
+        s.misc_u[3] = pks;
+        s.red_f[2] = ph;
+      }
+    }
+    __syncthreads();
+    hit = s.misc_u[1] != 0u;
+    c = s.red_f[1];
+    wrank = s.misc_u[2];
+    pks = s.misc_u[3];
+    ph = s.red_f[2];
+    __syncthreads();
+    bh = bl;
+  }
+  LUMEN_TICK("bv_cross", LUMEN_TIMING_ROW);
+  if (t < 64u) {
+    const ValHit h{hit, 0u, 0u, c};
     // the values around the crossing's with the same p (p is monotone in
     // the value, so they are adjacent among the values present)
     uint32_t hi = pks, lo = pks;
@@ -1801,7 +1945,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
     }
     if (lane == 0) {
       s.misc_u[0] = h.found ? 1u : 0u;
-      s.misc_u[1] = rank;
+      s.misc_u[1] = wrank;
       s.misc_u[2] = lo;
       s.misc_u[3] = hi;
       s.red_f[0] = c;
@@ -2089,9 +2233,12 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
   if ((P.flags & kTopP) && !small) {
     float m = kNegInf;
     uint32_t nan = 0;
-    // bf16 rows also count their values (top-p by distinct value)
+    // bf16 rows also count their values (top-p by distinct value): here,
+    // or (lumen_sample_rows_single, whose softmax sum takes lists A and B
+    // for its exp table) in a pass of their own after that sum
     const bool bf = !row.f;
-    if (bf) {
+    const bool count_now = bf && !V2;
+    if (count_now) {
       bv_clear(s);
       __syncthreads();
     }
@@ -2099,7 +2246,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       float x = v1f(v);
       m = rmax(m, x);
       nan |= is_nan(x) ? 1u : 0u;
-      if (bf) bv_count(x, s);
+      if (count_now) bv_count(x, s);
     });
     m = block_rmax(m, s);
     nan = block_or_u32(nan, s);
@@ -2127,7 +2274,34 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       // softmax sum at T = 1 and, for the window path, a key histogram of the
       // positive-probability tokens (bf16 rows walk their value counts
       // instead, and build it only if that walk cannot run)
-      auto e1f = [&](uint32_t, float v) -> float { return expf_glibc(__fsub_rn(v1f(v), m1)); };
+      // bf16 rows of lumen_sample_rows_single: exp(x - m1) from an LDS table
+      // (list A) over 64 binades of |value| per sign; live summands have x
+      // >= m1 - 128, so |x| <= W = max(|m1|, |m1 - 128|) and patterns above
+      // the window are zero, patterns below it take the direct computation
+      const bool tab1 = V2 && bf;
+      float* const T1 = reinterpret_cast<float*>(s.A);
+      uint32_t wlo1 = 0, whi1 = 0;
+      if (tab1) {
+        const float W = fmaxf(fabsf(m1), fabsf(__fsub_rn(m1, 128.f)));
+        uint32_t emax = ((__float_as_uint(W) >> 23) & 0xffu) + 1u;
+        emax = emax > 254u ? 254u : (emax < 63u ? 63u : emax);
+        wlo1 = (emax - 63u) << 7;
+        whi1 = (emax + 1u) << 7;
+#pragma unroll 1
+        for (uint32_t j = t; j < 16384u; j += kThreads) {
+          const float v = __uint_as_float((((j >> 13) << 15) | (wlo1 + (j & 8191u))) << 16);
+          T1[j] = expf_glibc(__fsub_rn(v1f(v), m1));
+        }
+        __syncthreads();
+      }
+      auto e1f = [&](uint32_t, float v) -> float {
+        if (tab1) {
+          const uint32_t p = __float_as_uint(v) >> 16, q = (p & 0x7fffu) - wlo1;
+          if (q < 8192u) return T1[q + ((p >> 15) << 13)];
+          if ((p & 0x7fffu) >= whi1) return 0.f;
+        }
+        return expf_glibc(__fsub_rn(v1f(v), m1));
+      };
       bool rec_ok = false;
       EcssResult e{0.f, 0, -1, 0.f};
       if (V2 && bf) e = row_rec_sum<false>(a, b, row, e1f, 0.f, s, rec_ok);
@@ -2148,6 +2322,14 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       S1 = e.c;
       tr.topp_sum = S1;
       LUMEN_TICK("rs_S1", b);
+      if (bf && !count_now) {
+        bv_clear(s);
+        __syncthreads();
+        row_foreach(row, [&](uint32_t, float v) { bv_count(v1f(v), s); });
+        __syncthreads();
+        tr.passes++;
+        LUMEN_TICK("rs_count", b);
+      }
       float c = 0.f;
       bool found = false;
       // bf16 rows: the walk over distinct values
