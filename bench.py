@@ -385,6 +385,8 @@ def measure(eng, name, steps, warmup, graph, rotate_bytes, cpu=True, cpu_budget=
         kern_ms = float(np.mean([a.elapsed_time(b) for a, b in zip(gs, ge)])) / graph
         mode = f"HIP graph replays of {graph} launches"
     logit_bytes = B * V * (2 if w.dtype == "bf16" else 4)
+    # one workgroup per row (lumen_sample_rows_single) once the rows fill the CUs
+    kernel = "lumen_sample_rows_single" if B >= 256 else "lumen_sample_rows"
     achieved = logit_bytes / (kern_ms * 1e-3) / 1e9
     # traces of one more call per buffer: passes and CDF values for parity
     traces = []
@@ -413,8 +415,8 @@ def measure(eng, name, steps, warmup, graph, rotate_bytes, cpu=True, cpu_budget=
                                  "not from the 256 MB Infinity Cache"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles(f"lumen_sample_rows_{name}_pmc.txt"),
-                     "kernel": "lumen_sample_rows", "kernel_ms": round(kern_ms, 5),
+                     "traffic": traffic_from_profiles(f"{kernel}_{name}_pmc.txt"),
+                     "kernel": kernel, "kernel_ms": round(kern_ms, 5),
                      "bytes_per_launch": logit_bytes},
         "logit_passes_per_row": {k: round(float(np.mean(v)), 2) for k, v in kinds.items()},
     }
