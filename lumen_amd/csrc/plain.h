@@ -109,8 +109,11 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
                               ? ei * exp((double)__fmul_rn(mi, invT) - (double)m3w) : 0.0;
       const double ps = wave_reduce(term, 0.0, [](double l, double r) { return l + r; });
       const bool anynan = __ballot(ni || (in && !(ei == ei))) != 0ull;
+      // an earlier slice holding the maximum has added exp(0) = 1
+      const bool one = __ballot(lane < vs && mi == m1w) != 0ull;
       if (lane == 0) {
         rowv[0] = m1w;
+        rowv[1] = one ? 1.f : 0.f;
         *reinterpret_cast<double*>(rowv + 2) = ps;
         rowu[1] = (anynan || !is_finite(m1w) || !is_finite(m3w)) ? 1u : 0u;
       }
@@ -118,6 +121,7 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
     __syncthreads();
     m3 = __fmul_rn(rowv[0], invT);
     const double p_slice = *reinterpret_cast<const double*>(rowv + 2);
+    const float lb_slice = rowv[1];
     bad = rowu[1] != 0u;
     __syncthreads();
     if (bad) break;
@@ -130,7 +134,7 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
           make_float4(x[4 * qq], x[4 * qq + 1], x[4 * qq + 2], x[4 * qq + 3]);
     __syncthreads();
     const uint32_t nthr = (sc.hi - sc.lo + kResK - 1u) / kResK;
-    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, vs), s);
+    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, vs), s, 0.f, lb_slice);
     if (t == 0) {
       ws.part_nrec[vs] = rc.ok ? rc.items : 0xffffffffu;
       ws.part_nraw[vs] = rc.raws;
@@ -210,7 +214,9 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
   if (good) {
     if (t < 64u) res_walk<true>(Gv, nit, rawbase, rdraw, nullptr, s);
     __syncthreads();
-    good = s.misc_u[0] != 0u;
+    // the records skip threads surely past the draw: no hit means the
+    // chunked method decides
+    good = s.misc_u[0] != 0u && s.misc_u[1] != 0u;
   }
   if (!good) {
 #ifdef LUMEN_FALLBACK_DEBUG

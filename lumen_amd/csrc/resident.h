@@ -203,7 +203,7 @@ struct RecCount {
 template <bool FIND = false>
 __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, uint32_t pos0,
                                                uint32_t nthr, uint32_t* rec, Smem& s,
-                                               float probe = 0.f) {
+                                               float probe = 0.f, float lb = 0.f) {
   const uint32_t t = threadIdx.x;
   const bool live = t < nthr;
   const float4* e4 = reinterpret_cast<const float4*>(et);  // this thread's 32 summands (LDS)
@@ -216,8 +216,38 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
     d += (double)f.z;
     d += (double)f.w;
   }
-  double tot;
-  const double P = p_slice + block_excl_scan_f64(d, s, &tot);
+  // the f64 prefix of the thread totals (the estimated running sum at the
+  // thread's start) and, with it, a floor for the exact running sum there:
+  // a sum of non-negative f32 terms is never below any term added so far,
+  // so max(lb, the largest summand of the threads before) bounds it (a
+  // row's maximum adds exactly 1.0, a binade edge the estimate straddles)
+  float mx = 0.f;
+#pragma unroll
+  for (int m = 0; m < (int)kResK; ++m) mx = fmaxf(mx, et[m]);
+  const uint32_t lane = t & 63u, w = t >> 6;
+  const double dinc = wave_scan_incl(d, 0.0, [](double l, double r) { return l + r; });
+  const float minc = wave_scan_incl(mx, 0.f, [](float l, float r) { return fmaxf(l, r); });
+  double* wsum_d = s.wsum;
+  float* wsum_m = s.red_f;
+  if (lane == 63u) {
+    wsum_d[w] = dinc;
+    wsum_m[w] = minc;
+  }
+  __syncthreads();
+  double pre = 0.0, tot = 0.0;
+  float mpre = 0.f;
+#pragma unroll
+  for (uint32_t i = 0; i < (uint32_t)kWaves; ++i) {
+    const double x = wsum_d[i];
+    if (i < w) {
+      pre += x;
+      mpre = fmaxf(mpre, wsum_m[i]);
+    }
+    tot += x;
+  }
+  __syncthreads();
+  const double P = p_slice + pre + (dinc - d);
+  const double floor_t = (double)fmaxf(fmaxf(lb, mpre), wave_shr1(minc, 0.f));
 #ifdef LUMEN_TIMING
   LUMEN_TICK("rr_scan", LUMEN_TIMING_ROW);
 #endif
@@ -227,11 +257,16 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   // by up to ~4e-9 of it per element
   constexpr double kProbeRel = 1e-4;
   const double rel = FIND ? kProbeRel : 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
-  const uint32_t blo = est_binade(P * (1.0 - rel));
+  const uint32_t blo = est_binade(fmax(P * (1.0 - rel), floor_t));
   const uint32_t bhi = est_binade((P + d) * (1.0 + rel));
-  bool unc = live && blo != bhi;
+  // a search: a thread whose running sum surely starts above the probe
+  // cannot hold the hit and records nothing (a walk that then finds no hit
+  // fails, and the caller takes the chunked method)
+  const bool past = FIND && live && P * (1.0 - 1e-4) > (double)probe;
+  const bool act = live && !past;
+  bool unc = act && blo != bhi;
   if (FIND)
-    unc = unc || (live && P * (1.0 - kProbeRel) <= (double)probe && (double)probe <= (P + d) * (1.0 + kProbeRel));
+    unc = unc || (act && P * (1.0 - kProbeRel) <= (double)probe && (double)probe <= (P + d) * (1.0 + kProbeRel));
   const uint32_t bin = unc ? est_binade(P + 0.5 * d) : blo;
   float y0 = __uint_as_float(bin), y1 = __uint_as_float(bin | 1u);
 #pragma unroll
@@ -251,20 +286,20 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   // neighbours' classes: a binade (low 23 bits zero), uncertain or absent
   constexpr uint32_t kUnc = 1u, kDead = 2u;
   uint32_t* cls = s.H0;
-  const uint32_t code = !live ? kDead : unc ? kUnc : bin;
+  const uint32_t code = !act ? kDead : unc ? kUnc : bin;
   cls[t] = code;
   __syncthreads();
   const uint32_t prv = t > 0 ? cls[t - 1] : kDead;
   const uint32_t nxt = t + 1 < (uint32_t)kThreads ? cls[t + 1] : kDead;
   // a run starts after anything else (certain threads never change binade
   // without an uncertain thread between them) and ends before anything else
-  const bool head = live && (unc || prv != code);
-  const bool last = live && !unc && nxt != code;
+  const bool head = act && (unc || prv != code);
+  const bool last = act && !unc && nxt != code;
 #ifdef LUMEN_TIMING
   LUMEN_TICK("rr_maps", LUMEN_TIMING_ROW);
 #endif
   SegVal prev;
-  const SegVal inc = seg_scan_incl(SegVal{head ? 1u : 0u, (live && !unc) ? own : PMap{0u, 0u}},
+  const SegVal inc = seg_scan_incl(SegVal{head ? 1u : 0u, (act && !unc) ? own : PMap{0u, 0u}},
                                    s.ecss, s.est, &prev);
   const uint32_t packed = ((unc || last) ? 1u : 0u) | ((unc ? 1u : 0u) << 16);
   uint32_t ptot;
@@ -724,9 +759,12 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
       const uint32_t cin = wave_scan_incl(ci, 0u, op_add_u32);
       const uint32_t nc = wave_read(cin, 63);
       const bool nan = __ballot(in && !(ei == ei)) != 0ull;
+      // an earlier slice holding the maximum has added exp(0) = 1
+      const bool one = __ballot(lane < vs && mi == m1w) != 0ull;
       if (lane == vs) rowu[2] = cin - ci;
       if (lane == 0) {
         rowv[0] = m1w;
+        rowv[1] = one ? 1.f : 0.f;
         *reinterpret_cast<double*>(rowv + 2) = ps;
         rowu[0] = nc;
         rowu[1] = (nan || !is_finite(m1w) || nc > (uint32_t)kCandCap) ? 1u : 0u;
@@ -735,6 +773,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     __syncthreads();
     m1 = rowv[0];
     const double p_slice = *reinterpret_cast<const double*>(rowv + 2);
+    const float lb_slice = rowv[1];
     const uint32_t cbase = rowu[2];
     bad = !ok || rowu[1] != 0u;
     __syncthreads();
@@ -794,7 +833,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     for (uint32_t i = t; i < kBins; i += kThreads) hg[i] = hl[i];
     LUMEN_TICK("rb_hist", b);
     const uint32_t nthr = (sc.hi - sc.lo + kResK - 1u) / kResK;
-    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, vs), s);
+    const RecCount rc = res_record(Lt, p_slice, sc.lo, nthr, res_rec(a, b, vs), s, 0.f, lb_slice);
     if (t == 0) {
       ws.part_nrec[vs] = rc.ok ? rc.items : 0xffffffffu;
       ws.part_nraw[vs] = rc.raws;

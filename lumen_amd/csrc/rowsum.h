@@ -66,12 +66,17 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
   const double rel = 5e-5 + 4e-9 * (double)(pos0 + t * kResK + kResK);
   const uint32_t blo = est_binade(P * (1.0 - rel));
   const uint32_t bhi = est_binade((P + d) * (1.0 + rel));
-  bool unc = live && blo != bhi;
+  // a search: a thread whose running sum surely starts above the probe
+  // cannot hold the hit and records nothing (a walk that then finds no hit
+  // fails, and the caller takes the chunked method)
+  const bool past = FIND && live && P * (1.0 - 1e-4) > (double)probe;
+  const bool act = live && !past;
+  bool unc = act && blo != bhi;
   // the probe's margin is the drift of a probability sum from its estimate
   // (the exact softmax sum divided out): observed up to ~3e-5 of it
   constexpr double kProbeRel = 1e-4;
   if (FIND)
-    unc = unc || (live && P * (1.0 - kProbeRel) <= (double)probe && (double)probe <= (P + d) * (1.0 + kProbeRel));
+    unc = unc || (act && P * (1.0 - kProbeRel) <= (double)probe && (double)probe <= (P + d) * (1.0 + kProbeRel));
   const uint32_t bin = unc ? est_binade(P + 0.5 * d) : blo;
   float y0 = __uint_as_float(bin), y1 = __uint_as_float(bin | 1u);
 #pragma unroll
@@ -84,7 +89,7 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
   // 2. class codes of the neighbours (runs are maximal spans of certain
   // threads in one binade)
   constexpr uint32_t kUnc = 1u, kDead = 2u;
-  const uint32_t code = !live ? kDead : unc ? kUnc : bin;
+  const uint32_t code = !act ? kDead : unc ? kUnc : bin;
   uint32_t* bc = s.H0 + 64;  // [kWaves][2]: first and last code of each wave
   if (lane == 0u) bc[2u * w] = code;
   if (lane == 63u) bc[2u * w + 1u] = code;
@@ -93,13 +98,13 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
   if (lane == 0u) prv = w > 0u ? bc[2u * w - 1u] : kDead;
   uint32_t nxt = (uint32_t)__shfl_down((int)code, 1);
   if (lane == 63u) nxt = w + 1u < (uint32_t)kWaves ? bc[2u * w + 2u] : kDead;
-  const bool head = live && (unc || prv != code);
-  const bool last = live && !unc && nxt != code;
+  const bool head = act && (unc || prv != code);
+  const bool last = act && !unc && nxt != code;
   const uint32_t packed = ((unc || last) ? 1u : 0u) | ((unc ? 1u : 0u) << 16);
   // 3. the segmented scan of the run maps and the scan of the item / raw
   // counts, wave by wave, then across the waves
   const SegVal id{0u, PMap{0u, 0u}};
-  const SegVal sinc = wave_scan_incl(SegVal{head ? 1u : 0u, (live && !unc) ? own : PMap{0u, 0u}}, id,
+  const SegVal sinc = wave_scan_incl(SegVal{head ? 1u : 0u, (act && !unc) ? own : PMap{0u, 0u}}, id,
                                      seg_combine);
   const uint32_t pinc = wave_scan_incl(packed, 0u, op_add_u32);
   uint32_t* st = s.H0 + 128;  // [kWaves][4]: head, a0, a1, count total
@@ -281,8 +286,9 @@ __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, co
   __syncthreads();
   LUMEN_TICK("rr_walk", b);
   const bool found = s.misc_u[1] != 0u;
-  // a search cut short must have found its hit
-  ok = s.misc_u[0] != 0u && (found || nb == nblk);
+  // a search must have found its hit (its records skip threads surely
+  // past the probe, and it may have stopped early)
+  ok = s.misc_u[0] != 0u && (found || !FIND);
   const uint32_t hk = s.misc_u[2], hj = s.misc_u[3];
   r.c = s.red_f[0];
   r.before = s.red_f[1];
