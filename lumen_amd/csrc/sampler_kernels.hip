@@ -284,6 +284,18 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, Smem& s) {
   return r;
 }
 
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, Smem& s) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_reduce(v, 0u, [](uint32_t l, uint32_t r) { return l > r ? l : r; });
+  if (lane == 0) s.red_a[w] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) r = s.red_a[i] > r ? s.red_a[i] : r;
+  __syncthreads();
+  return r;
+}
+
 __device__ __forceinline__ uint32_t block_or_u32(uint32_t v, Smem& s) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   v = wave_reduce(v, 0u, op_or_u32);
@@ -1779,13 +1791,13 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
                                                        float m1, float S1,
                                                        float top_p, Smem& s, RowTrace& tr,
                                                        uint32_t& pk_lo, uint32_t& pk_hi,
-                                                       uint32_t& istar) {
+                                                       uint32_t& istar, uint32_t ncount) {
   const uint32_t t = threadIdx.x, V = row.V;
   const uint32_t* cw = bv_counts(s);
   auto vf = [kmask, kcut](uint32_t, float v) -> float {
     return (kmask && tkey(v) < kcut) ? kNegInf : v;
   };
-  if (V > (1u << 22) || !bv_blocks(V, s)) return -1;
+  if (V > (1u << 22) || !bv_blocks(ncount, s)) return -1;
   __syncthreads();
   auto pof = [&](uint32_t pk) { return __fdiv_rn(expf_glibc(__fsub_rn(bv_value(pk), m1)), S1); };
   // The walk in rounds of at most 1024 present values (descending), every
@@ -2242,14 +2254,37 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       bv_clear(s);
       __syncthreads();
     }
-    row_foreach(row, [&](uint32_t i, float v) {
-      float x = v1f(v);
-      m = rmax(m, x);
-      nan |= is_nan(x) ? 1u : 0u;
-      if (count_now) bv_count(x, s);
-    });
-    m = block_rmax(m, s);
-    nan = block_or_u32(nan, s);
+    if (V2 && bf && !kmask) {
+      // lumen_sample_rows_single, bf16 without a top-k mask: the largest
+      // total_cmp key of the non-NaN values (integer max, no NaN cases); a
+      // maximum of +-0 is then taken again with f32::max semantics
+      uint32_t kmax = 0x007fu;  // -inf
+      row_foreach(row, [&](uint32_t, float v) {
+        const uint32_t p = __float_as_uint(v) >> 16;
+        const uint32_t sg = (uint32_t)((int32_t)(p << 16) >> 31);
+        const uint32_t k = (p ^ (sg | 0x8000u)) & 0xffffu;
+        const bool isn = (p & 0x7fffu) > 0x7f80u;
+        nan |= isn ? 1u : 0u;
+        kmax = isn ? kmax : max(kmax, k);
+      });
+      kmax = block_max_u32(kmax, s);
+      nan = block_or_u32(nan, s);
+      m = bv_value(kmax);
+      if (m == 0.f) {
+        m = kNegInf;
+        row_foreach(row, [&](uint32_t, float v) { m = rmax(m, v); });
+        m = block_rmax(m, s);
+      }
+    } else {
+      row_foreach(row, [&](uint32_t i, float v) {
+        float x = v1f(v);
+        m = rmax(m, x);
+        nan |= is_nan(x) ? 1u : 0u;
+        if (count_now) bv_count(x, s);
+      });
+      m = block_rmax(m, s);
+      nan = block_or_u32(nan, s);
+    }
     tr.passes++;
     LUMEN_TICK("rs_topp_max", b);
     m1 = m;
@@ -2280,6 +2315,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       // the window are zero, patterns below it take the direct computation
       const bool tab1 = V2 && bf;
       float* const T1 = reinterpret_cast<float*>(s.A);
+      uint32_t* const cc1 = reinterpret_cast<uint32_t*>(s.Bk);  // [8192]
       uint32_t wlo1 = 0, whi1 = 0;
       if (tab1) {
         const float W = fmaxf(fabsf(m1), fabsf(__fsub_rn(m1, 128.f)));
@@ -2292,19 +2328,36 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
           const float v = __uint_as_float((((j >> 13) << 15) | (wlo1 + (j & 8191u))) << 16);
           T1[j] = expf_glibc(__fsub_rn(v1f(v), m1));
         }
+        for (uint32_t j = t; j < 8192u; j += kThreads) cc1[j] = 0u;
         __syncthreads();
       }
+      // Without a top-k mask the sum also counts the values it reads, as u16
+      // pairs by table entry (list B): patterns above the window are zero
+      // summands (never part of the walk), and any live pattern below it
+      // makes the row count in a pass of its own.
+      const bool fuse = tab1 && !kmask;
+      uint32_t ndead = 0, ntiny = 0;
       auto e1f = [&](uint32_t, float v) -> float {
         if (tab1) {
           const uint32_t p = __float_as_uint(v) >> 16, q = (p & 0x7fffu) - wlo1;
-          if (q < 8192u) return T1[q + ((p >> 15) << 13)];
-          if ((p & 0x7fffu) >= whi1) return 0.f;
+          if (q < 8192u) {
+            const uint32_t j = q + ((p >> 15) << 13);
+            if (fuse) atomicAdd(&cc1[j >> 1], 1u << ((j & 1u) << 4));
+            return T1[j];
+          }
+          if ((p & 0x7fffu) >= whi1) {
+            ndead += fuse ? 1u : 0u;
+            return 0.f;
+          }
+          ntiny += fuse ? 1u : 0u;
         }
         return expf_glibc(__fsub_rn(v1f(v), m1));
       };
       bool rec_ok = false;
       EcssResult e{0.f, 0, -1, 0.f};
       if (V2 && bf) e = row_rec_sum<false>(a, b, row, e1f, 0.f, s, rec_ok);
+      // (the chunked method below reads the same summands; its counts are
+      // not used)
       if (!rec_ok) {
         clear_hist(s.H0, 2048);
         __syncthreads();
@@ -2322,12 +2375,41 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       S1 = e.c;
       tr.topp_sum = S1;
       LUMEN_TICK("rs_S1", b);
+      uint32_t ncount = V;  // elements the value counts hold
       if (bf && !count_now) {
-        bv_clear(s);
-        __syncthreads();
-        row_foreach(row, [&](uint32_t, float v) { bv_count(v1f(v), s); });
-        __syncthreads();
-        tr.passes++;
+        bool fused = false;
+        if (fuse && rec_ok) {
+          ndead = block_sum_u32(ndead, s);
+          fused = block_sum_u32(ntiny, s) == 0u;
+        }
+        if (fused) {
+          // the table-entry counts, moved to the layout of the value walk
+          uint32_t w8[8];
+#pragma unroll
+          for (uint32_t k = 0; k < 8u; ++k) w8[k] = cc1[8u * t + k];
+          __syncthreads();
+          bv_clear(s);
+          __syncthreads();
+          uint32_t* cw = bv_counts(s);
+#pragma unroll
+          for (uint32_t k = 0; k < 16u; ++k) {
+            const uint32_t c = (w8[k >> 1] >> ((k & 1u) << 4)) & 0xffffu;
+            if (c) {
+              const uint32_t j = 16u * t + k;
+              const uint32_t pat = ((j >> 13) << 15) | (wlo1 + (j & 8191u));
+              const uint32_t pk = (pat ^ ((uint32_t)((int32_t)(pat << 16) >> 31) | 0x8000u)) & 0xffffu;
+              atomicAdd(&cw[pk >> 1], c << ((pk & 1u) << 4));
+            }
+          }
+          __syncthreads();
+          ncount = V - ndead;
+        } else {
+          bv_clear(s);
+          __syncthreads();
+          row_foreach(row, [&](uint32_t, float v) { bv_count(v1f(v), s); });
+          __syncthreads();
+          tr.passes++;
+        }
         LUMEN_TICK("rs_count", b);
       }
       float c = 0.f;
@@ -2335,7 +2417,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       // bf16 rows: the walk over distinct values
       const int byval = !bf ? -1
                             : topp_by_value(row, kmask, kcut, m1, S1, P.top_p, s, tr, pk_lo, pk_hi,
-                                            istar);
+                                            istar, ncount);
       LUMEN_TICK("rs_byval", b);
       if (bf && byval < 0) {
         // the window path's key histogram, skipped above
