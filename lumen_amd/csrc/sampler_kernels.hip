@@ -2869,7 +2869,12 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
 //  * top-p rows use one row barrier and a chain in which slice sl waits for
 //    the exact running sum of slice sl-1. Every wait is bounded; on timeout
 //    the row reports a failure instead of waiting further.
-// All workgroups of a launch are co-resident (cooperative launch).
+// The launch is an ordinary one (cooperative only with LUMEN_SAMPLER_COOP):
+// the host sizes the grid to the resident capacity (one workgroup per CU),
+// so a row's workgroups are co-resident unless other streams' kernels hold
+// CUs. Then a waiting workgroup spins up to kSpinLimit s_sleep periods
+// (about 100 ms) before its row takes the single-workgroup path: correct,
+// but slow.
 
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr uint32_t kSampleN = 4096;

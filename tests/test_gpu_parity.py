@@ -615,6 +615,56 @@ def test_device_decode_state(eng, V):
     assert [int(v) for v in st] == [r.state() for r in host_rng]
 
 
+def test_device_ring_wrap_against_oracle(eng):
+    # A ring of 8 tokens over 24 decode steps, so it wraps three times:
+    # windows below the ring (3), equal to it (8) and the whole history
+    # (repeat_last_n 0, which grows past the ring and is carried by the
+    # token-by-token count updates). Every step's tokens and the penalized
+    # logits are checked against the oracle's Sampler::sample loop
+    # (sampling.rs:429-433: sample_logits, then record), with the reference
+    # RNG advanced only by sampled rows.
+    import torch
+    from lumen_amd.sampling import DeviceDecodeState
+    from oracle import oracle as o
+
+    V, cap, steps = 500, 8, 24
+    params = [SP(temperature=0.8, repetition_penalty=1.3, repeat_last_n=3),
+              SP(temperature=0.0, frequency_penalty=1.0, repeat_last_n=8),
+              SP(temperature=0.9, top_k=40, presence_penalty=0.8, repeat_last_n=0),
+              SP(temperature=1.1, repetition_penalty=1.2, min_p=0.05, repeat_last_n=5)]
+    B = len(params)
+    seeds = [71, 72, 73, 74]
+    rng = np.random.default_rng(17)
+    prompt = [rng.integers(0, V, size=3).astype(np.uint32) for _ in range(B)]
+    ds = DeviceDecodeState(eng, seeds, cap=cap, histories=prompt)
+    orngs = [o.Xorshift64(sd) for sd in seeds]
+    hist = [list(int(x) for x in p_) for p_ in prompt]
+    for step in range(steps):
+        lg = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+        for b in range(B):
+            lg[b, hist[b][-4:]] += 3.0
+        x = torch.from_numpy(lg).to("cuda:0")
+        pen = torch.empty((B, V), dtype=torch.float32, device="cuda:0")
+        log(f"case ring wrap step {step}")
+        _, got = ds.step(eng, x, params, penalized_out=pen)
+        pen_h = pen.cpu().numpy()
+        for b in range(B):
+            op = parity.to_oracle_params(params[b])
+            want_pen = o.apply_penalties(lg[b].copy(), op, hist[b]) if (
+                params[b].penalties_active() and hist[b]) else lg[b]
+            assert np.array_equal(pen_h[b].view(np.uint32),
+                                  np.asarray(want_pen, np.float32).view(np.uint32)), (step, b)
+            want = o.sample_logits(lg[b], op, hist[b], orngs[b])
+            assert got[b] == want, (step, b, got[b], want)
+            hist[b].append(int(want))
+    lens = ds.lens.cpu().numpy()
+    ring = ds.ring.cpu().numpy().view(np.uint32)
+    for b in range(B):
+        assert lens[b] == len(hist[b])
+        for k in range(len(hist[b]) - cap, len(hist[b])):
+            assert ring[b, k % cap] == hist[b][k]
+
+
 def test_device_history_rewrite(eng):
     # counts updated token by token across calls, then the ring rewritten by
     # the caller (a new prompt, a new epoch): the counts are made again, and
