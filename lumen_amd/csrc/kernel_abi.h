@@ -79,13 +79,10 @@ constexpr int kMassBins = 512;      // top-p window planning bins
 constexpr int kChainMaxQ = 2;       // sub-chunks per slice in the softmax-sum chain
 constexpr int kRowRecs = kMaxSlices * kChainMaxQ * 16;  // run records per row (one per wave segment)
 constexpr int kRecWords = 1152;     // words per run record slot
-// Records of the exact row sums of lumen_sample_rows_single (row_rec_sum):
-// per row, one area of kRsBlockWords words per block of kResSlice logits
-// (at most kMaxSlices blocks), items first, raw summands from kRsRawOff.
-constexpr uint32_t kRsBlockWords = 4096;
-constexpr uint32_t kRsItemCap = 512;   // items (4 words each) per block
-constexpr uint32_t kRsRawOff = 2048;
-constexpr uint32_t kRsRawCap = 64;     // raws (32 words each) per block
+// Records of the exact row sums of lumen_sample_rows_single (row_rec_sum),
+// kept in LDS: per block of kResSlice logits at most
+constexpr uint32_t kRsItemCap = 512;   // items (4 words each)
+constexpr uint32_t kRsRawCap = 64;     // raws (32 words each)
 
 
 // Per-row coordination block in device memory. Zero at allocation; the last
@@ -150,7 +147,6 @@ struct KernelArgs {
   uint32_t* est;             // [B][kRowRecs][kRecWords] run records of wave segments
   uint64_t* cand;            // [B][kCandCap] candidate buffers
   float* hist;               // [B][kMaxSlices][kMassBins] candidate exp-mass per logit bin
-  uint32_t* rsum;            // [B][kMaxSlices][kRsBlockWords] row_rec_sum records (single-workgroup launches)
   uint32_t slices;           // workgroups per row (G) when blk_map is NULL
   uint32_t xcd_rows;         // 1: place all slices of a row on one XCD (blk_map NULL)
   // Per-block placement: (row << 10) | (G << 5) | slice, or kIdleBlock. Rows
@@ -201,11 +197,11 @@ struct KernelArgs {
 // object whose stamp differs from its own: kernel arguments read with
 // another layout would be garbage pointers. kAbiVersion changes with any
 // change of meaning that keeps the sizes.
-constexpr uint32_t kAbiVersion = 6;
+constexpr uint32_t kAbiVersion = 7;
 constexpr uint32_t kAbiStamp =
     (kAbiVersion * 0x9E3779B1u) ^ ((uint32_t)sizeof(KernelArgs) * 0x85EBCA77u) ^
     ((uint32_t)sizeof(RowWs) * 0xC2B2AE3Du) ^ ((uint32_t)sizeof(RowParams) * 0x27D4EB2Fu) ^
-    ((uint32_t)sizeof(RowTrace) * 0x165667B1u) ^ (kRsBlockWords * 0xD3A2646Cu) ^
+    ((uint32_t)sizeof(RowTrace) * 0x165667B1u) ^ (kRsItemCap * 0xD3A2646Cu) ^
     ((uint32_t)kCandStride * 0xFD7046C5u) ^ ((uint32_t)kRowRecs * 0xB55A4F09u);
 
 }  // namespace lumen

@@ -11,7 +11,7 @@
 //    holds the 32 contiguous summands 32t .. 32t+31 in registers;
 //  - each block writes its record (runs of threads whose binade the f64
 //    estimate fixes, as parity maps, and the raw summands of the others) to
-//    the row's own record area (KernelArgs::rsum), one area per block;
+//    row's records in LDS (s.H: items from the bottom, raws from the top);
 //  - one walk on wave 0 over all records gives the exact result.
 // Its LDS needs are the record walk's (s.H), the class codes (s.H0) and the
 // scan scratch, so it runs beside the bf16 value counts held in lists A and
@@ -21,13 +21,12 @@
 
 namespace lumen {
 
-// Block blk's record area of row b.
-__device__ __forceinline__ uint32_t* rs_rec(const KernelArgs& a, int b, uint32_t blk) {
-  return a.rsum + ((uint64_t)b * kMaxSlices + blk) * kRsBlockWords;
-}
+// LDS words of a row's records (all of s.H).
+constexpr uint32_t kRsLdsWords = 4096;
 
-// res_record for summands held in registers, into an area of kRsBlockWords
-// words (at most kRsItemCap items, kRsRawCap raws); also returns the
+// res_record for summands held in registers, into the row's records in s.H
+// (at most kRsItemCap items and kRsRawCap raws per block, kRsLdsWords words
+// per row; ibase / rbase: the items and raws before this block); also returns the
 // block's f64 total (the estimate of the next block's start). Three
 // barriers: the f64 prefix, the neighbours' class codes at wave edges, and
 // the wave totals of the segmented run scan and of the item / raw counts
@@ -36,7 +35,8 @@ __device__ __forceinline__ uint32_t* rs_rec(const KernelArgs& a, int b, uint32_t
 // so consecutive calls need none in between.
 template <bool FIND>
 __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], double p_slice,
-                                                    uint32_t pos0, uint32_t nthr, uint32_t* rec,
+                                                    uint32_t pos0, uint32_t nthr, uint32_t ibase,
+                                                    uint32_t rbase,
                                                     Smem& s, float probe, double* tot_out) {
   const uint32_t t = threadIdx.x, lane = t & 63u, w = t >> 6;
   const bool live = t < nthr;
@@ -130,20 +130,24 @@ __device__ __forceinline__ RecCount res_record_regs(const float (&e)[kResK], dou
   const SegVal inc = seg_combine(spre, sinc);
   const uint32_t pos = ppre + pinc - packed;
   RecCount rc{ptot & 0xffffu, ptot >> 16, true};
-  if (rc.items > kRsItemCap || rc.raws > kRsRawCap) {
+  if (rc.items > kRsItemCap || rc.raws > kRsRawCap ||
+      4u * (ibase + rc.items) + kResK * (rbase + rc.raws) > kRsLdsWords) {
     rc.ok = false;
     return rc;
   }
-  const uint32_t ip = pos & 0xffffu, rp = pos >> 16;
+  // items from the bottom of s.H, raw slot r at the top (kResK words ending
+  // kResK * r below it)
+  const uint32_t ip = ibase + (pos & 0xffffu), rg = rbase + (pos >> 16);
+  u32x4* items = reinterpret_cast<u32x4*>(s.H);
   if (unc) {
-    gst(reinterpret_cast<u32x4*>(rec + 4u * ip), u32x4{bin, own.a0, own.a1, FIND ? rp | (t << 16) : rp});
-    u32x4* raw = reinterpret_cast<u32x4*>(rec + kRsRawOff + kResK * rp);
+    items[ip] = u32x4{bin, own.a0, own.a1, FIND ? rg | (t << 16) : rg};
+    u32x4* raw = reinterpret_cast<u32x4*>(s.H + kRsLdsWords - kResK * (rg + 1u));
 #pragma unroll
     for (int m = 0; m < (int)kResK / 4; ++m)
-      gst(raw + m, u32x4{__float_as_uint(e[4 * m]), __float_as_uint(e[4 * m + 1]),
-                         __float_as_uint(e[4 * m + 2]), __float_as_uint(e[4 * m + 3])});
+      raw[m] = u32x4{__float_as_uint(e[4 * m]), __float_as_uint(e[4 * m + 1]),
+                     __float_as_uint(e[4 * m + 2]), __float_as_uint(e[4 * m + 3])};
   } else if (last) {
-    gst(reinterpret_cast<u32x4*>(rec + 4u * ip), u32x4{bin, inc.m.a0, inc.m.a1, kNoRaw});
+    items[ip] = u32x4{bin, inc.m.a0, inc.m.a1, kNoRaw};
   }
   return rc;
 }
@@ -184,58 +188,11 @@ __device__ __forceinline__ void row_load32(const Row& row, uint32_t i0, float (&
   }
 }
 
-// The records of the G blocks gathered into s.H (at most 4096 words; ib, rb
-// in s.H0 + [0, 64)); false when they do not fit.
-__device__ __forceinline__ bool rec_gather_small(const KernelArgs& a, int b, uint32_t G,
-                                                 const uint32_t* nrec, const uint32_t* nraw,
-                                                 Smem& s, uint32_t* nit_out, uint32_t* rawbase_out) {
-  const uint32_t t = threadIdx.x, lane = t & 63u;
-  uint32_t* ib = s.H0;
-  uint32_t* rb = s.H0 + 32;
-  if (t < 64u) {
-    const bool in = lane < G;
-    const uint32_t ni = in ? nrec[lane] : 0u;
-    const uint32_t nr = in ? nraw[lane] : 0u;
-    const uint32_t ei = wave_scan_incl(ni, 0u, op_add_u32);
-    const uint32_t er = wave_scan_incl(nr, 0u, op_add_u32);
-    const uint32_t pi = wave_shr1(ei, 0u), pr = wave_shr1(er, 0u);
-    if (lane <= G) {
-      ib[lane] = pi;
-      rb[lane] = pr;
-    }
-  }
-  __syncthreads();
-  const uint32_t nit = ib[G], nrw = rb[G];
-  const uint32_t rawbase = 4u * nit;
-  const uint32_t nw = rawbase + kResK * nrw;
-  __syncthreads();
-  if (nw > 4096u) return false;
-  uint32_t* words = s.H;
-  for (uint32_t f = t; f < nw; f += kThreads) {
-    uint32_t i = 0;
-    const uint32_t* src;
-    if (f < rawbase) {
-      const uint32_t it = f >> 2;
-      while (i + 1u < G && ib[i + 1] <= it) ++i;
-      src = rs_rec(a, b, i) + 4u * (it - ib[i]) + (f & 3u);
-    } else {
-      const uint32_t r = (f - rawbase) / kResK;
-      while (i + 1u < G && rb[i + 1] <= r) ++i;
-      src = rs_rec(a, b, i) + kRsRawOff + kResK * (r - rb[i]) + (f - rawbase) % kResK;
-    }
-    words[f] = gld(src);
-  }
-  __syncthreads();
-  *nit_out = nit;
-  *rawbase_out = rawbase;
-  return true;
-}
-
 // The exact sequential sum of xf(i, v) over the row in index order (FIND
 // false), or the first element whose running sum exceeds probe (FIND true:
 // found, pos, the sums before and at it). The summands must be finite and
-// >= 0. ok = false: the method could not finish (nothing is wrong), or the
-// launch has no record area.
+// >= 0. ok = false: the method could not finish (nothing is wrong). The
+// records live in s.H (at most kRsLdsWords words for the whole row).
 template <bool FIND, class XF>
 __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, const Row& row,
                                                   XF&& xf, float probe, Smem& s, bool& ok) {
@@ -243,12 +200,12 @@ __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, co
   const uint32_t nblk = (V + kResSlice - 1u) / kResSlice;
   EcssResult r{0.f, 0, -1, 0.f};
   ok = false;
-  if (!a.rsum || nblk == 0u || nblk > (uint32_t)kMaxSlices) return r;
-  uint32_t* nrec = s.H0 + 1040;  // [kMaxSlices]
-  uint32_t* nraw = s.H0 + 1056;  // [kMaxSlices]
+  if (nblk == 0u || nblk > (uint32_t)kMaxSlices) return r;
+  uint32_t* ioff = s.H0 + 1040;  // [kMaxSlices] each block's first item
   double P = 0.0;
   bool fit = true;
   uint32_t nb = nblk;  // blocks recorded
+  uint32_t ibase = 0, rbase = 0;  // items and raws recorded so far
   for (uint32_t blk = 0; blk < nblk; ++blk) {
     const uint32_t lo = blk * kResSlice;
     const uint32_t n = min(kResSlice, V - lo);
@@ -261,15 +218,15 @@ __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, co
     }
     LUMEN_TICK("rr_x", b);
     double tot;
-    const RecCount rc = res_record_regs<FIND>(e, P, lo, (n + kResK - 1u) / kResK, rs_rec(a, b, blk),
-                                              s, probe, &tot);
+    const RecCount rc = res_record_regs<FIND>(e, P, lo, (n + kResK - 1u) / kResK, ibase, rbase, s,
+                                              probe, &tot);
     P += tot;
     LUMEN_TICK("rr_rec", b);
-    if (t == 0) {
-      nrec[blk] = rc.items;
-      nraw[blk] = rc.raws;
-    }
+    if (t == 0) ioff[blk] = ibase;
     fit = fit && rc.ok;
+    if (!fit) break;
+    ibase += rc.items;
+    rbase += rc.raws;
     // searching: once the running sum is surely above the probe where the
     // next block starts, the hit lies in the blocks recorded so far
     if (FIND && blk + 1u < nblk &&
@@ -279,8 +236,27 @@ __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, co
     }
   }
   __syncthreads();
-  uint32_t nit = 0, rawbase = 0;
-  if (!fit || !rec_gather_small(a, b, nb, nrec, nraw, s, &nit, &rawbase)) return r;
+  if (!fit) return r;
+  // the raws, moved to follow the items in slot order (the walk's layout),
+  // and the blocks' item offsets (raw slots are numbered across the row)
+  const uint32_t nit = ibase, rawbase = 4u * nit, rw = kResK * rbase;
+  uint32_t mv[kRsLdsWords / kThreads];
+#pragma unroll
+  for (uint32_t k = 0; k < kRsLdsWords / kThreads; ++k) {
+    const uint32_t f = t + k * kThreads;
+    mv[k] = f < rw ? s.H[kRsLdsWords - kResK * (f / kResK + 1u) + f % kResK] : 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t k = 0; k < kRsLdsWords / kThreads; ++k) {
+    const uint32_t f = t + k * kThreads;
+    if (f < rw) s.H[rawbase + f] = mv[k];
+  }
+  if (t < 32u) {
+    s.H0[t] = t < nb ? ioff[t] : nit;
+    s.H0[32u + t] = 0u;
+  }
+  __syncthreads();
   LUMEN_TICK("rr_gather", b);
   if (t < 64u) res_walk_at<FIND>(nb, nit, rawbase, probe, s.H, s);
   __syncthreads();

@@ -190,7 +190,6 @@ struct lumen_sampler {
   DevBuf ws;    // [B] RowWs, zeroed at allocation, self-resetting afterwards
   DevBuf cand;  // [B][kCandStride] candidate buffers
   DevBuf est;   // [B][kRowRecs][kRecWords] run records of the split top-p path
-  DevBuf rsum;  // [B][kMaxSlices][kRsBlockWords] records of lumen_sample_rows_single's row sums
   DevBuf hist;  // [B][kMaxSlices][kMassBins] candidate mass histograms
   DevBuf guard;  // [B][kGuardWords] anti-restate candidates when the caller passes none
   uint32_t* guard_dev = nullptr;  // where the last call's candidates went
@@ -600,7 +599,6 @@ void lumen_sampler_destroy(lumen_sampler* s) {
   if (s->ws.p) (void)hipFree(s->ws.p);
   if (s->cand.p) (void)hipFree(s->cand.p);
   if (s->est.p) (void)hipFree(s->est.p);
-  if (s->rsum.p) (void)hipFree(s->rsum.p);
   if (s->hist.p) (void)hipFree(s->hist.p);
   if (s->guard.p) (void)hipFree(s->guard.p);
   if (s->wcnt.p) (void)hipFree(s->wcnt.p);
@@ -965,18 +963,6 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
       hipError_t e =
           hipModuleLaunchCooperativeKernel(s->fn, nblocks, 1, 1, 1024, 1, 1, 0, st, params);
       return hip_fail(e);
-    }
-  }
-  if (G == 1) {
-    // one workgroup per row: lumen_sample_rows_single, with the record area
-    // of its exact row sums (row_rec_sum); without one it sums in chunks
-    const size_t rsum_bytes = sizeof(uint32_t) * lumen::kRsBlockWords * lumen::kMaxSlices * B;
-    if (noalloc) {
-      ka.rsum = static_cast<uint32_t*>(arena.take(rsum_bytes));
-    } else {
-      int rc = ensure_dev(s->rsum, rsum_bytes, st);
-      if (rc != LUMEN_OK) return rc;
-      ka.rsum = static_cast<uint32_t*>(s->rsum.p);
     }
   }
   size_t argsz = sizeof(ka);
