@@ -1787,6 +1787,7 @@ __device__ __forceinline__ float bv_value(uint32_t pk) {
 // The row and the top-k mask (kmask: keys below kcut read as -inf) come by
 // value: in a non-inlined function, state reached through references would
 // be reloaded from private memory on every element.
+template <bool V2>
 __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask, uint32_t kcut,
                                                        float m1, float S1,
                                                        float top_p, Smem& s, RowTrace& tr,
@@ -1840,6 +1841,45 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
     const int bl = s.misc_i[0];
     __syncthreads();
     LUMEN_TICK("bv_plan", LUMEN_TIMING_ROW);
+    uint32_t n;
+    if (V2) {
+    // compaction of the present values of blocks (bl, bh], descending: wave
+    // w takes the key offsets [w * wspan, (w + 1) * wspan) below khi, 512
+    // per step, each lane 8 consecutive keys (one 16-byte read of 4 count
+    // words), placed by a wave scan of the lanes' counts
+    const uint32_t khi = (uint32_t)(bh + 1) * 256u, klo = (uint32_t)(bl + 1) * 256u;
+    const uint32_t span = khi - klo, wspan = (span + 512u * kWaves - 1u) / (512u * kWaves) * 512u;
+    auto group = [&](uint32_t off0) -> u32x4 {  // the 4 words of keys khi-1-off0 .. khi-8-off0
+      return off0 < span ? *reinterpret_cast<const u32x4*>(cw + ((khi - 8u - off0) >> 1))
+                         : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto nz = [](uint32_t x) { return ((x & 0xffffu) != 0u ? 1u : 0u) + ((x >> 16) != 0u ? 1u : 0u); };
+    uint32_t mine = 0;
+    for (uint32_t q = 0; q < wspan; q += 512u) {
+      const u32x4 g = group(w * wspan + q + 8u * lane);
+      mine += wave_reduce(nz(g.x) + nz(g.y) + nz(g.z) + nz(g.w), 0u, op_add_u32);
+    }
+    uint32_t at = block_excl_scan_u32(lane == 0 ? mine : 0u, s, &n);
+    at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
+    for (uint32_t q = 0; q < wspan && mine; q += 512u) {
+      const uint32_t off0 = w * wspan + q + 8u * lane;
+      const u32x4 g = group(off0);
+      const uint32_t cl = nz(g.x) + nz(g.y) + nz(g.z) + nz(g.w);
+      const uint32_t incl = wave_scan_incl(cl, 0u, op_add_u32);
+      uint32_t pos = at + incl - cl;
+      const uint32_t wd[4] = {g.w, g.z, g.y, g.x};  // descending keys: high word, high half first
+#pragma unroll
+      for (uint32_t k = 0; k < 8u; ++k) {
+        const uint32_t cnt = (wd[k >> 1] >> ((1u - (k & 1u)) << 4)) & 0xffffu;
+        if (cnt) {
+          if (pos < 1024u) list[pos] = ((khi - 1u - off0 - k) << 16) | cnt;
+          ++pos;
+        }
+      }
+      at += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    }
+    __syncthreads();
+    } else {
     // compaction of the present values of blocks (bl, bh], descending: wave
     // w takes keys khi - 1 - [w * wspan, (w + 1) * wspan), 64 consecutive
     // keys per step (one per lane), and places them by ballot
@@ -1850,7 +1890,6 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
       const uint32_t off = w * wspan + q + lane;
       mine += (uint32_t)__popcll(__ballot(off < span && vcount(cw, khi - 1u - off) != 0u));
     }
-    uint32_t n;
     uint32_t at = block_excl_scan_u32(lane == 0 ? mine : 0u, s, &n);
     at = (uint32_t)__builtin_amdgcn_readfirstlane((int)at);
     for (uint32_t q = 0; q < wspan && mine; q += 64u) {
@@ -1863,6 +1902,7 @@ __device__ __attribute__((noinline)) int topp_by_value(const Row row, bool kmask
       at += (uint32_t)__popcll(bm);
     }
     __syncthreads();
+    }
     if (n > 1024u) n = 1024u;  // cannot happen: the plan bounds the round
     LUMEN_TICK("bv_list", LUMEN_TIMING_ROW);
     // every wave: its values' p, the f64 estimate of its start, its map
@@ -2416,7 +2456,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
       bool found = false;
       // bf16 rows: the walk over distinct values
       const int byval = !bf ? -1
-                            : topp_by_value(row, kmask, kcut, m1, S1, P.top_p, s, tr, pk_lo, pk_hi,
+                            : topp_by_value<V2>(row, kmask, kcut, m1, S1, P.top_p, s, tr, pk_lo, pk_hi,
                                             istar, ncount);
       LUMEN_TICK("rs_byval", b);
       if (bf && byval < 0) {
