@@ -398,6 +398,13 @@ def test_bf16_topp_by_value(eng):
     params.append(SP(temperature=1.0, top_p=0.5))
     rows.append(rng.integers(-4, 5, V) * 0.5)                     # tied maxima kept whole at T = 1
     params.append(SP(temperature=1.0, top_p=0.9))
+    # a maximum of +0 and -0 (the key maximum is taken again with f32::max
+    # semantics), exact zeros below the exp table's window
+    z = np.minimum(rng.normal(0, 1, V), 0.0)
+    z[rng.random(V) < 0.2] = 0.0
+    z[rng.random(V) < 0.2] = -0.0
+    rows.append(z)
+    params.append(SP(temperature=1.0, top_p=0.9))
     bits = to_bf16_bits(np.array(rows, dtype=np.float32))
     f32 = (bits.astype(np.uint32) << 16).view(np.float32)
     B = len(rows)
