@@ -2122,6 +2122,13 @@ template <bool FIND, class XF>
 __device__ __forceinline__ EcssResult row_rec_sum(const KernelArgs& a, int b, const Row& row,
                                                   XF&& xf, float probe, Smem& s, bool& ok);
 
+// exp(x - m), out of line: the rare elements of a table-driven sum that
+// fall outside the table (inlined into every unrolled summand, its code
+// made the single-workgroup sampler spill in its hot loops)
+__device__ __attribute__((noinline)) float exp_sub_outline(float x, float m) {
+  return expf_glibc(__fsub_rn(x, m));
+}
+
 // The whole sampler for row b, run by one workgroup: row_single<false> is the
 // fallback of the split paths inside lumen_sample_rows, row_single<true> the
 // body of lumen_sample_rows_single (one workgroup per row), whose full-row
@@ -2391,7 +2398,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
           }
           ntiny += fuse ? 1u : 0u;
         }
-        return expf_glibc(__fsub_rn(v1f(v), m1));
+        return V2 ? exp_sub_outline(v1f(v), m1) : expf_glibc(__fsub_rn(v1f(v), m1));
       };
       bool rec_ok = false;
       EcssResult e{0.f, 0, -1, 0.f};
@@ -2857,7 +2864,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
         if ((p & 0x7fffu) >= whi) return 0.f;
       }
       const float w = wf(i, v);
-      return w == kNegInf ? 0.f : expf_glibc(__fsub_rn(w, m3));
+      return w == kNegInf ? 0.f : V2 ? exp_sub_outline(w, m3) : expf_glibc(__fsub_rn(w, m3));
     };
     bool rec_ok = false;
     EcssResult S{0.f, 0, -1, 0.f};
@@ -2884,7 +2891,7 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
         if ((p & 0x7fffu) >= whi) return 0.f;
       }
       const float w = wf(i, v);
-      return __fdiv_rn(w == kNegInf ? 0.f : expf_glibc(__fsub_rn(w, m3)), S3);
+      return __fdiv_rn(w == kNegInf ? 0.f : V2 ? exp_sub_outline(w, m3) : expf_glibc(__fsub_rn(w, m3)), S3);
     };
     EcssResult e{0.f, 0, -1, 0.f};
     rec_ok = false;
