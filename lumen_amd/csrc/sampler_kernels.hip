@@ -2135,7 +2135,7 @@ __device__ __attribute__((noinline)) float exp_sub_outline(float x, float m) {
 // exact sums take the record method (row_rec_sum). Two instantiations keep
 // the register allocation of the split kernel independent of the latter.
 template <bool V2>
-__device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b, Smem& s) {
+__device__ __forceinline__ void row_single_body(const KernelArgs& a, int b, Smem& s) {
   const int t = threadIdx.x;
   const RowParams P = a.inline_rows ? a.inline_params[b] : a.params[b];
   const uint32_t V = a.vocab;
@@ -2904,6 +2904,13 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
     tok = e.found ? (uint32_t)e.pos : V - 1;
   }
   write_result(a, b, tok, tr);
+}
+
+// The split kernel's fallback: out of line, so that its registers do not
+// weigh on the split paths. lumen_sample_rows_single inlines the body.
+template <bool V2>
+__device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b, Smem& s) {
+  row_single_body<V2>(a, b, s);
 }
 
 
@@ -4208,7 +4215,7 @@ extern "C" __global__ void __launch_bounds__(1024) lumen_sample_rows_single(Kern
   if (b >= a.batch) return;
   LUMEN_TICK_SLOT(b, 0u);
   __syncthreads();
-  row_single<true>(a, (int)b, s);
+  row_single_body<true>(a, (int)b, s);
 }
 
 // Penalty window counts from the device history ring, one workgroup per row
