@@ -469,7 +469,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(rows are independent; see DESIGN.md for how the path would shard)",
+              "(rows are independent: N GPUs would each take B/N of the rows)",
               file=sys.stderr)
         sys.exit(2)
 
