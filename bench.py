@@ -188,11 +188,14 @@ def b1_latency(eng, draws=10_000, api_draws=2_000):
             float(np.percentile(np.array(api), 50)))
 
 
-def b1_decode_device_state(eng, draws=2_000):
-    """Config 2 as a decode loop with the state on the device: the history
-    ring (whole-history penalty window, counted on the device each draw) and
-    the Xorshift64 state live in HBM; per draw one call (the window-count
-    kernel and the sampler) and a 4-byte readback."""
+def b1_decode_device_state(eng, draws=10_000):
+    """Config 2 as its configuration states it: `draws` sequential draws from
+    the fixed seed with the history growing by each drawn token
+    (Sampler::sample, sampling.rs:429-433: draw, then record). The history
+    ring (whole-history penalty window, its counts updated on the device each
+    draw) and the Xorshift64 state live in HBM; per draw one call (the
+    window-count kernel and the sampler) and a 4-byte readback. Returns the
+    latencies and the drawn tokens."""
     import torch
 
     from lumen_amd.sampling import DeviceDecodeState
@@ -202,15 +205,49 @@ def b1_decode_device_state(eng, draws=2_000):
     dev = torch.from_numpy(w.logits).cuda()
     ds = DeviceDecodeState(eng, w.seeds, cap=8192, histories=w.histories)
     tok = torch.empty(1, dtype=torch.int32, device=dev.device)
-    times = []
-    for i in range(draws + 50):
+    times, drawn = [], []
+    for i in range(draws):
         t0 = time.perf_counter()
-        ds.step(eng, dev, w.params, tokens_out=tok, sync=True)
+        _, host = ds.step(eng, dev, w.params, tokens_out=tok, sync=True)
         t1 = time.perf_counter()
+        drawn.append(int(host[0]))
         if i >= 50:
             times.append((t1 - t0) * 1e6)
     times = np.array(times)
-    return float(np.percentile(times, 50)), float(np.percentile(times, 99)), len(times)
+    return float(np.percentile(times, 50)), float(np.percentile(times, 99)), len(times), drawn
+
+
+def b1_decode_parity(drawn, threads):
+    """The oracle's Sampler::sample loop beside the device decode loop (outside
+    any timed region): step i is the oracle's sample_logits on the history
+    prompt + drawn[:i] with the i-th draw of Xorshift64(seed). While the two
+    loops agree, that is exactly the oracle's own loop, so the steps are
+    checked in parallel; the first mismatch is reported with the count."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from lumen_amd.workloads import config2
+    from oracle import oracle as o
+
+    w = config2()
+    op = oracle_params(w)[0]
+    rng = o.Xorshift64(w.seeds[0])
+    rs = [rng.next_f32() for _ in drawn]
+    hist = np.concatenate([np.asarray(w.histories[0], np.uint32),
+                           np.asarray(drawn, np.uint32)])
+    h0 = len(w.histories[0])
+    row = w.logits[0]
+
+    def one(i):
+        return o.sample_logits_r(row, op, hist[:h0 + i], rs[i])[0]
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        want = list(ex.map(one, range(len(drawn))))
+    bad = [i for i, (g, r) in enumerate(zip(drawn, want)) if g != r]
+    return {"steps": len(drawn), "match": len(drawn) - len(bad), "mismatch": len(bad),
+            "first_mismatch_step": bad[0] if bad else None,
+            "distinct_tokens": len(set(drawn)), "history_at_end": h0 + len(drawn),
+            "oracle_threads": threads, "oracle_s": round(time.perf_counter() - t0, 1)}
 
 
 def b1_graph_decode(eng, per_graph=32, replays=20):
@@ -388,16 +425,23 @@ def measure(eng, name, steps, warmup, graph, rotate_bytes, cpu=True, cpu_budget=
     # one workgroup per row (lumen_sample_rows_single) once the rows fill the CUs
     kernel = "lumen_sample_rows_single" if B >= 256 else "lumen_sample_rows"
     achieved = logit_bytes / (kern_ms * 1e-3) / 1e9
-    # traces of one more call per buffer: passes and CDF values for parity
-    traces = []
-    for d, t in zip(devs, toks):
+    # the tokens the timed launches wrote (each buffer's last timed launch),
+    # copied before anything else runs
+    tok_host = [t.cpu().numpy().view(np.uint32).copy() for t in toks]
+    # traces of one more call per buffer, into token buffers of their own:
+    # passes and CDF values for the parity report
+    traces, trace_toks = [], []
+    for d in devs:
         tr = torch.zeros((B, 16), dtype=torch.int32, device="cuda")
-        eng.sample_batch(d, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=t,
+        tt = torch.empty(B, dtype=torch.int32, device="cuda")
+        eng.sample_batch(d, w.params, penalty_counts=csr, uniforms_dev=u_dev, tokens_out=tt,
                          trace=tr, sync=False)
         traces.append(tr)
+        trace_toks.append(tt)
     torch.cuda.synchronize()
     traces = [tr.cpu().numpy().view(np.uint32) for tr in traces]
-    tok_host = [t.cpu().numpy().view(np.uint32) for t in toks]
+    traced_same = all(np.array_equal(a, t.cpu().numpy().view(np.uint32))
+                      for a, t in zip(tok_host, trace_toks))
     kinds = {}
     for b, p in enumerate(w.params):
         kinds.setdefault(row_kind(p), []).append(int(traces[0][b, 13]))
@@ -422,6 +466,8 @@ def measure(eng, name, steps, warmup, graph, rotate_bytes, cpu=True, cpu_budget=
     }
     nt = host_cores()
     res["parity"] = parity_check(w, lgs, tok_host, traces, u_host, nt)
+    res["parity"]["tokens_checked"] = "the timed launches' own tokens"
+    res["parity"]["traced_call_same_tokens"] = bool(traced_same)
     if cpu:
         rate, rows, reps, cel = cpu_baseline(w, u_host, budget_s=cpu_budget)
         res["cpu_baseline"] = {"value": round(rate, 2), "unit": "samples/s", "cores": 1,
@@ -529,11 +575,14 @@ def main():
             "us_per_token": round(us, 2), "tokens": n,
             "workload": "config2 decode steps (device RNG and history ring) captured 32 to a "
                         "HIP graph; wall time per token over graph replays"}
-        p50, p99, n = b1_decode_device_state(eng)
+        p50, p99, n, drawn = b1_decode_device_state(eng, args.b1_draws)
         line["b1_decode_device_state"] = {
-            "p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": n,
-            "workload": "config2 decode loop: RNG state and a 8192-token history ring on "
-                        "the device, whole-history penalty window counted per draw"}
+            "p50_us": round(p50, 2), "p99_us": round(p99, 2), "draws": len(drawn),
+            "timed_draws": n,
+            "workload": "config2 as configured: sequential draws from the fixed seed, the "
+                        "history (4,096 prompt ids) growing by each drawn token; RNG state "
+                        "and the history ring on the device, whole-history penalty window",
+            "parity": b1_decode_parity(drawn, host_cores())}
     if not args.no_configs:
         line["configs"] = {}
         for name, steps in (("config1", 200), ("config4", 40), ("config5", 100),
