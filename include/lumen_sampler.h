@@ -253,6 +253,23 @@ int lumen_sampler_sample_batch_noalloc(lumen_sampler *s, const lumen_batch *batc
 int lumen_sampler_sample_batch_sync(lumen_sampler *s, const lumen_batch *batch,
                                     uint32_t *tokens_host, lumen_stream stream);
 
+/* Bound of every cross-workgroup wait inside a launch, in microseconds of
+ * the device wall clock (default 2000). A row's workgroups wait for each
+ * other at a few points; they are co-resident when the call has the GPU to
+ * itself, but kernels of other streams can hold CUs. A wait that reaches the
+ * bound gives up, is counted (lumen_sampler_wait_timeouts) and its row is
+ * resolved by the exact single-workgroup path: the token is the same, the
+ * call slower. 0 makes every such wait give up at once. Applies to the
+ * following calls on the context. No counterpart in the reference, whose
+ * CPU sampler has no cross-workgroup waits; it plays the part of its GPU
+ * path's visible fallback (cuda/backend_impl.rs:1276-1293). */
+int lumen_sampler_set_wait_limit(lumen_sampler *s, uint32_t microseconds);
+
+/* Number of cross-workgroup waits that gave up since the context was
+ * created (see lumen_sampler_set_wait_limit). Reads device memory: call it
+ * once the calls to count have completed. */
+int lumen_sampler_wait_timeouts(lumen_sampler *s, uint64_t *count);
+
 /* Range checks of the server's wire layer
  * (crates/lumen-server/src/wire/openai.rs:357-381): temperature must be
  * finite and in [0, 2], top_p finite and in [0, 1]. Returns LUMEN_OK or LUMEN_ERR_INVALID, and

@@ -35,6 +35,8 @@ EXPORTS = (
     "lumen_xorshift64_next_u64",
     "lumen_xorshift64_next_f32",
     "lumen_sampler_version",
+    "lumen_sampler_set_wait_limit",
+    "lumen_sampler_wait_timeouts",
     "lumen_sampler_last_error",
     "lumen_sampling_params_validate",
     "lumen_anti_restate_select",
@@ -167,6 +169,10 @@ def load():
     L.lumen_xorshift64_next_u64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
     L.lumen_xorshift64_next_f32.restype = ctypes.c_float
     L.lumen_xorshift64_next_f32.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    L.lumen_sampler_set_wait_limit.restype = ctypes.c_int
+    L.lumen_sampler_set_wait_limit.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+    L.lumen_sampler_wait_timeouts.restype = ctypes.c_int
+    L.lumen_sampler_wait_timeouts.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64)]
     L.lumen_sampler_version.restype = ctypes.c_char_p
     L.lumen_sampler_version.argtypes = []
     L.lumen_sampler_last_error.restype = ctypes.c_char_p

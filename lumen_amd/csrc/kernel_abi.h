@@ -156,7 +156,12 @@ struct KernelArgs {
   uint32_t inline_rows;      // > 0: params come from inline_params
   uint32_t inline_draws;     // != 0: draws come from inline_uniforms
   uint32_t count_cap;        // form C: count entries per row (ring_cap, or vocab for long windows)
-  uint32_t pad2;
+  // Bound of every cross-workgroup wait, in ticks of the 100 MHz wall clock;
+  // 0 makes every such wait give up at once. A wait that gives up adds 1 to
+  // *timeouts (device memory of the context) and its row takes the exact
+  // single-workgroup path.
+  uint32_t wait_ticks;
+  uint32_t* timeouts;
   // Synchronous calls: the token is also written to pinned host memory
   // mapped into the device, and *done_mapped (host memory) counts the rows
   // written, so the host waits on that count instead of a copy and a stream
@@ -197,7 +202,7 @@ struct KernelArgs {
 // object whose stamp differs from its own: kernel arguments read with
 // another layout would be garbage pointers. kAbiVersion changes with any
 // change of meaning that keeps the sizes.
-constexpr uint32_t kAbiVersion = 7;
+constexpr uint32_t kAbiVersion = 8;
 constexpr uint32_t kAbiStamp =
     (kAbiVersion * 0x9E3779B1u) ^ ((uint32_t)sizeof(KernelArgs) * 0x85EBCA77u) ^
     ((uint32_t)sizeof(RowWs) * 0xC2B2AE3Du) ^ ((uint32_t)sizeof(RowParams) * 0x27D4EB2Fu) ^

@@ -83,7 +83,7 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
     }
   }
   wg_arrive(&ws.bar, 0xffffffffu, s);
-  bool ok = wg_wait_geq(&ws.bar, G, s);
+  bool ok = wg_wait_geq(a, &ws.bar, G, s);
 
   // ---- phase B: the last chunk first (its logits are in registers) ----
   float m3 = 0.f;
@@ -166,7 +166,7 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
     }
     __syncthreads();
   } else {
-    ok = wg_wait_geq(&ws.bar, 2u * G, s);
+    ok = wg_wait_geq(a, &ws.bar, 2u * G, s);
     if (!ok && t == 0) __hip_atomic_fetch_or(&ws.status, 8u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // ---- phase C: the CDF records; chunk sl*q first (its summands are in

@@ -560,6 +560,123 @@ __device__ __forceinline__ void res_walk_at(uint32_t G, uint32_t nit, uint32_t r
   }
 }
 
+// res_walk_at with the running sum kept as a uniform value and no branch per
+// run item: every lane loads its item of the current 64 (and the raw
+// summands of an uncertain thread) up front, so a run costs one parity
+// select, one add and its checks, and an uncertain thread that must be
+// replayed is replayed by all lanes at once, each on its own item's
+// summands from the same exact start, lane q's result being the one kept.
+// Same results and outputs as res_walk_at; failed checks accumulate into a
+// flag tested once per 64 items.
+template <bool FIND>
+__device__ __forceinline__ void res_walk_fast(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
+                                              const uint32_t* words, Smem& s,
+                                              float* starts = nullptr) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t* ib = s.H0;
+  const uint32_t* rb = s.H0 + 32;
+  const uint4* items = reinterpret_cast<const uint4*>(words);
+  const float* raws = reinterpret_cast<const float*>(words + rawbase);
+  uint32_t cb = 0u, bad = 0u, found = 0u, hit_k = 0u, hit_j = 0u, before = 0u;
+  uint32_t ns = 0;  // next slice whose start is still to be recorded
+  for (uint32_t k0 = 0; k0 < nit; k0 += 64u) {
+    const uint32_t k = k0 + lane;
+    uint4 it = make_uint4(0u, 0u, 0u, kNoRaw);
+    uint32_t roff = kNoRaw;
+    if (k < nit) {
+      it = items[k];
+      if (it.w != kNoRaw) {
+        uint32_t i = 0;
+        while (i + 1u < G && ib[i + 1] <= k) ++i;
+        roff = kResK * (rb[i] + (it.w & 0xffffu));
+      }
+    }
+    float xr[kResK];
+    {
+      const float4* r4 = reinterpret_cast<const float4*>(raws + (roff == kNoRaw ? 0u : roff));
+#pragma unroll
+      for (int m = 0; m < (int)kResK / 4; ++m) {
+        const float4 f = roff == kNoRaw ? make_float4(0.f, 0.f, 0.f, 0.f) : r4[m];
+        xr[4 * m] = f.x;
+        xr[4 * m + 1] = f.y;
+        xr[4 * m + 2] = f.z;
+        xr[4 * m + 3] = f.w;
+      }
+    }
+    const uint32_t cnt = min(64u, nit - k0);
+    for (uint32_t q = 0; q < cnt; ++q) {
+      if (!FIND && starts) {
+        while (ns < G && ib[ns] <= k0 + q) {
+          if (lane == 0) starts[ns] = __uint_as_float(cb);
+          ++ns;
+        }
+      }
+      const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
+      const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
+      const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
+      const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
+      const uint32_t inc = (cb & 1u) ? a1 : a0;
+      // the map applies: the exact sum is inside its binade and stays there
+      // (and, searching, stays at or below r)
+      const bool fits = (cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u &&
+                        !(FIND && r < __uint_as_float(cb + inc));
+      if (ro == kNoRaw) {
+        // a run: the crossing cannot lie in it, so a map that does not
+        // apply is a failed check
+        bad |= fits ? 0u : 1u;
+        cb = fits ? cb + inc : cb;
+        continue;
+      }
+      if (fits) {
+        cb += inc;
+        continue;
+      }
+      // an uncertain thread replayed from the exact start
+      float c = __uint_as_float(cb), cbef = c;
+      uint32_t hj = kResK;
+#pragma unroll
+      for (int j = 0; j < (int)kResK; ++j) {
+        const float y = __fadd_rn(c, xr[j]);
+        if (FIND) {
+          const bool h = hj == kResK && r < y;
+          cbef = h ? c : cbef;
+          hj = h ? (uint32_t)j : hj;
+        }
+        c = y;
+      }
+      if (FIND) {
+        const uint32_t hq = (uint32_t)__builtin_amdgcn_readlane((int)hj, (int)q);
+        if (hq < kResK) {
+          // the hit sum: the add at hj from the sum before it
+          const float cb4 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cbef), (int)q));
+          found = 1u;
+          hit_k = k0 + q;
+          hit_j = hq;
+          before = __float_as_uint(cb4);
+          cb = __float_as_uint(__fadd_rn(cb4, raws[ro + hq]));
+          break;
+        }
+      }
+      cb = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(c), (int)q);
+    }
+    if (bad || found) break;
+  }
+  if (!FIND && !bad && starts) {
+    while (ns < G) {
+      if (lane == 0) starts[ns] = __uint_as_float(cb);
+      ++ns;
+    }
+  }
+  if (lane == 0) {
+    s.misc_u[0] = bad ? 0u : 1u;
+    s.misc_u[1] = found;
+    s.misc_u[2] = hit_k;
+    s.misc_u[3] = hit_j;
+    s.red_f[0] = __uint_as_float(cb);
+    s.red_f[1] = __uint_as_float(before);
+  }
+}
+
 // res_walk_at over the records gathered into s.Bk (res_gather).
 template <bool FIND>
 __device__ __forceinline__ void res_walk(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
@@ -611,21 +728,39 @@ __device__ __forceinline__ uint32_t res_chunks(uint32_t V, uint32_t G) {
 __device__ __forceinline__ void res_s1_walker(const KernelArgs& a, int b, uint32_t G, uint32_t Gv,
                                               Smem& s) {
   RowWs& ws = a.ws[b];
-  const bool ok = wg_wait_geq(&ws.arrive, G, s);
+  LUMEN_TICK("w_start", b);
+  const bool ok = wg_wait_geq(a, &ws.arrive, G, s);
+  LUMEN_TICK("w_waited", b);
   uint32_t nit = 0, rawbase = 0;
   bool good = ok && __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u &&
               res_gather(a, b, Gv, s, &nit, &rawbase);
+  LUMEN_TICK("w_gathered", b);
   if (good) {
-    if (threadIdx.x < 64u) res_walk<false>(Gv, nit, rawbase, 0.f, nullptr, s);
+    if (threadIdx.x < 64u)
+      res_walk_fast<false>(Gv, nit, rawbase, 0.f, reinterpret_cast<const uint32_t*>(s.Bk), s);
     __syncthreads();
     good = s.misc_u[0] != 0u;
   }
+  LUMEN_TICK("w_walked", b);
+#ifdef LUMEN_TIMING
+  if (threadIdx.x == 0 && b == LUMEN_TIMING_ROW)
+    printf("walker row %d: items %u raws %u\n", b, nit, s.H0[32 + Gv]);
+#endif
   if (threadIdx.x == 0) {
     if (good)
       ws.unused0 = __float_as_uint(s.red_f[0]);
     else
       __hip_atomic_fetch_or(&ws.status, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(&ws.bar, G, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t old = __hip_atomic_fetch_add(&ws.bar, G, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (old >= kAbandoned) {
+      // the finisher stopped waiting (a timed-out wait) and went on alone;
+      // this release is the row's last access to its block, so the walker
+      // restores it for the next call
+      ws.arrive = 0;
+      ws.bar = 0;
+      ws.cand_n = 0;
+      ws.status = 0;
+    }
   }
 }
 
@@ -717,7 +852,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   }
 #endif
   wg_arrive(&ws.bar, 0xffffffffu, s);
-  const bool ok = wg_wait_geq(&ws.bar, G, s);
+  const bool ok = wg_wait_geq(a, &ws.bar, G, s);
   if (!ok && t == 0) __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("r_barrier", b);
 #ifdef LUMEN_RES_STOP
@@ -864,12 +999,19 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   // gather, every load issued before any store: the summed mass histogram
   // into s.H, the candidates (logit bits << 32) | id into list A, and the
   // upper bound of S1 from the slices' estimates
+  uint32_t ej[kPer];  // exp(v - m1) of candidates kPer*t .. kPer*t + kPer-1
   {
     uint64_t cv[kPer];
+    const uint32_t* cande = reinterpret_cast<const uint32_t*>(cand + kCandCap);
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
       const uint32_t f = t + (uint32_t)q * kThreads;
       cv[q] = f < ncand ? cand[f] : 0ull;
+    }
+#pragma unroll
+    for (int q = 0; q < (int)kPer; ++q) {
+      const uint32_t f = kPer * t + (uint32_t)q;
+      ej[q] = f < ncand ? cande[f] : 0u;
     }
     float hs = 0.f;
     if (t < kBins) {
@@ -930,14 +1072,7 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   // position, orders like its id); candidates 8t .. 8t+7 per thread
   // (contiguous, so one block scan keeps index order)
   uint32_t wmask = 0;
-  uint32_t ej[kPer];
   {
-    const uint32_t* cande = reinterpret_cast<const uint32_t*>(cand + kCandCap);
-#pragma unroll
-    for (int q = 0; q < (int)kPer; ++q) {
-      const uint32_t f = kPer * t + (uint32_t)q;
-      ej[q] = f < ncand ? cande[f] : 0u;
-    }
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
       const float e = __uint_as_float(ej[q]);
@@ -964,10 +1099,21 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   LUMEN_TICK("r_sorted", b);
   RES_STOP(7);
   // S1 from the walker (always released, also on failure)
-  const bool got = wg_wait_geq(&ws.bar, 2u * Gr, s);
+  const bool got = wg_wait_geq(a, &ws.bar, 2u * Gr, s);
   if (t == 0) {
-    s.misc_u[2] = __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s.red_f[0] = __uint_as_float(ws.unused0);
+    if (got) {
+      s.misc_u[2] = __hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s.red_f[0] = __uint_as_float(ws.unused0);
+    } else {
+      // giving up on the walker: whichever of the two touches the row's
+      // block last restores it. A walker that has not released yet finds
+      // the mark and resets; otherwise this workgroup does, as usual. After
+      // the mark this workgroup no longer reads or writes the block.
+      const uint32_t old =
+          __hip_atomic_fetch_add(&ws.bar, kAbandoned, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      if (old < 2u * Gr) s.finisher = 0u;
+      s.misc_u[2] = 1u;
+    }
   }
   __syncthreads();
   const float S1 = s.red_f[0];
@@ -989,9 +1135,11 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
       s.Bk[j] = ((uint64_t)(~__float_as_uint(p)) << 32) | (uint32_t)k;
     }
     __syncthreads();
+    LUMEN_TICK("x_p", b);
     for (uint32_t j = t; j + 1u < nw; j += kThreads) swap |= s.Bk[j] > s.Bk[j + 1u] ? 1u : 0u;
     swap = block_or_u32(swap, s);
     if (swap) sort_u64_asc(s.Bk, nw, wtmp, s);
+    LUMEN_TICK(swap ? "x_resorted" : "x_inorder", b);
   }
   const float p_x = __fdiv_rn(e_lo, S1);  // every token outside the window has p <= p_x
   const EcssResult wk = list_ecss_block(
@@ -1021,14 +1169,13 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   uint32_t nk;
   {
     const uint32_t kmask = (kbits[t >> 2] >> (8u * (t & 3u))) & 0xffu;  // candidates 8t .. 8t+7
-    const uint32_t* cande = reinterpret_cast<const uint32_t*>(cand + kCandCap);
     uint64_t cv[kPer];
     uint32_t ev[kPer];
 #pragma unroll
     for (int q = 0; q < (int)kPer; ++q) {
       const bool in = (kmask >> q) & 1u;
       cv[q] = in ? (cand_lds ? s.A[kPer * t + (uint32_t)q] : cand[kPer * t + (uint32_t)q]) : 0ull;
-      ev[q] = in && pre_exp ? cande[kPer * t + (uint32_t)q] : 0u;
+      ev[q] = in && pre_exp ? ej[q] : 0u;
     }
     uint32_t ko = block_excl_scan_u32((uint32_t)__popc(kmask), s, &nk);
 #pragma unroll
@@ -1049,6 +1196,9 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   tr.pad[0] = 0;
   tr.pad[1] = ncand | (nw << 16);
   LUMEN_TICK("r_kept", b);
+#ifdef LUMEN_TIMING
+  if (t == 0 && b == LUMEN_TIMING_ROW) printf("finisher row %d: ncand %u nw %u kept %u nk %u\n", b, ncand, nw, (uint32_t)wk.pos + 1u, nk);
+#endif
   RES_STOP(9);
   // the nucleus holds the row maximum m1 (the largest p)
   const uint32_t tok = final_on_list(a, P, nk, rdraw, s, tr, m1, pre_exp);

@@ -209,6 +209,10 @@ struct lumen_sampler {
   uint32_t* map_host = nullptr;  // [0] count, [1..] tokens
   uint32_t* map_dev = nullptr;
   uint32_t map_cap = 0;
+  // bound of each cross-workgroup wait (lumen_sampler_set_wait_limit) and
+  // the device count of waits that gave up
+  uint32_t wait_us = 2000;
+  uint32_t* timeouts_dev = nullptr;
 };
 
 namespace {
@@ -585,7 +589,32 @@ int lumen_sampler_create(lumen_sampler** out, int device) {
     delete s;
     return LUMEN_ERR_HIP;
   }
+  if (hipMalloc(reinterpret_cast<void**>(&s->timeouts_dev), 256) != hipSuccess ||
+      hipMemset(s->timeouts_dev, 0, 256) != hipSuccess) {
+    (void)hipGetLastError();
+    if (s->timeouts_dev) (void)hipFree(s->timeouts_dev);
+    (void)hipEventDestroy(s->staged);
+    (void)hipModuleUnload(s->module);
+    delete s;
+    return LUMEN_ERR_HIP;
+  }
   *out = s;
+  return LUMEN_OK;
+}
+
+int lumen_sampler_set_wait_limit(lumen_sampler* s, uint32_t microseconds) {
+  if (!s) return fail(LUMEN_ERR_INVALID, "null context");
+  s->wait_us = microseconds;
+  return LUMEN_OK;
+}
+
+int lumen_sampler_wait_timeouts(lumen_sampler* s, uint64_t* count) {
+  if (!s || !count) return fail(LUMEN_ERR_INVALID, "null context or count");
+  DeviceGuard g(s->device);
+  uint32_t n = 0;
+  const hipError_t e = hipMemcpy(&n, s->timeouts_dev, sizeof n, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e);
+  *count = n;
   return LUMEN_OK;
 }
 
@@ -605,6 +634,7 @@ void lumen_sampler_destroy(lumen_sampler* s) {
   if (s->staged) (void)hipEventDestroy(s->staged);
   if (s->module) (void)hipModuleUnload(s->module);
   if (s->map_host) (void)hipHostFree(s->map_host);
+  if (s->timeouts_dev) (void)hipFree(s->timeouts_dev);
   delete s;
 }
 
@@ -752,6 +782,8 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   ka.tokens = bt->tokens;
   ka.trace = reinterpret_cast<lumen::RowTrace*>(bt->trace);
   ka.pen_out = bt->penalized_out;
+  ka.wait_ticks = (uint32_t)std::min<uint64_t>(100ull * s->wait_us, 0xffffffffull);
+  ka.timeouts = s->timeouts_dev;
 
   // Workgroups per row: enough to occupy every CU once (all co-resident),
   // at most kMaxSlices. With 8+ rows, a row's slices share one XCD.
@@ -805,6 +837,12 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
     // HIP stages before hipMemcpyAsync returns
     if (s->ids.size() > lumen::kNoAllocMaxCsr)
       return fail(LUMEN_ERR_INVALID, "noalloc: more than 65536 form-A penalty entries");
+    // a captured copy would read this host buffer at every replay, after
+    // later calls have refilled (or moved) it
+    if (capturing(st))
+      return fail(LUMEN_ERR_INVALID,
+                  "noalloc under stream capture: form-A histories (history_offsets) need a host "
+                  "copy; pass device penalty counts (pen_offsets) instead");
     s->img.assign(static_sz, 0);
     std::memcpy(s->img.data() + off_offs, s->offs.data(), sizeof(uint32_t) * (B + 1));
     if (!s->ids.empty()) {

@@ -87,8 +87,9 @@ __shared__ int g_nticks;
         if (g_tick_n[k_] > 0 && g_tick_t[k_][0] < t0_) t0_ = g_tick_t[k_][0];   \
       for (int k_ = 0; k_ < 16; ++k_)                                           \
         if (k_ != g_tick_slot && g_tick_n[k_] > 0)                              \
-          printf("tick[%d] last %s %f us\n", k_, g_tick_l[k_][g_tick_n[k_] - 1], \
-                 (double)(g_tick_t[k_][g_tick_n[k_] - 1] - t0_) / 100.0);       \
+          for (int i_ = (g_tick_n[k_] > 3 ? g_tick_n[k_] - 3 : 0); i_ < g_tick_n[k_]; ++i_) \
+          printf("tick[%d] %s %f us\n", k_, g_tick_l[k_][i_], \
+                 (double)(g_tick_t[k_][i_] - t0_) / 100.0);       \
       for (int i_ = 0; i_ < g_nticks; ++i_)                                     \
         printf("tick[%d] %s %f us\n", g_tick_slot, g_tick_l[g_tick_slot][i_],  \
                (double)(g_tick_t[g_tick_slot][i_] - t0_) / 100.0);              \
@@ -1010,12 +1011,16 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __uint_as_float((uint32_t)s.A[j]);
     __syncthreads();
     tr.final_max = known_max;
+    LUMEN_TICK("f_copy", LUMEN_TIMING_ROW);
     const EcssResult S = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssSum, 0.f, 0.f, s);
     const float S3 = S.c;
+    LUMEN_TICK("f_S", LUMEN_TIMING_ROW);
     for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
     __syncthreads();
+    LUMEN_TICK("f_div", LUMEN_TIMING_ROW);
     tr.final_sum = S3;
     const EcssResult e = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
+    LUMEN_TICK("f_find", LUMEN_TIMING_ROW);
     tr.cdf_before = e.found ? e.before : e.c;
     tr.cdf_at = e.c;
     if (e.found) return (uint32_t)(s.A[e.pos] >> 32);
@@ -2926,12 +2931,14 @@ __device__ __attribute__((noinline)) void row_single(const KernelArgs& a, int b,
 // The launch is an ordinary one (cooperative only with LUMEN_SAMPLER_COOP):
 // the host sizes the grid to the resident capacity (one workgroup per CU),
 // so a row's workgroups are co-resident unless other streams' kernels hold
-// CUs. Then a waiting workgroup spins up to kSpinLimit s_sleep periods
-// (about 100 ms) before its row takes the single-workgroup path: correct,
-// but slow.
+// CUs. Then a waiting workgroup gives up after KernelArgs::wait_ticks of the
+// 100 MHz wall clock (lumen_sampler_set_wait_limit; 2 ms by default), counts
+// the timeout in *KernelArgs::timeouts, and its row takes the exact
+// single-workgroup path: correct, slower, and visible to the caller.
 
-constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr uint32_t kSampleN = 4096;
+// bar value of a top-p row whose finisher stopped waiting for the S1 walker
+constexpr uint32_t kAbandoned = 1u << 24;
 
 struct Slice {
   uint32_t lo, hi;
@@ -2971,20 +2978,29 @@ __device__ __forceinline__ uint32_t wg_arrive(uint32_t* ctr, uint32_t last, Smem
   return old;
 }
 
-// Waits until *ctr >= target, then acquires. Returns false on timeout. The
-// counter is polled with relaxed loads (they read past this XCD's L2
-// without invalidating it); the one acquire comes after the wait.
-__device__ __forceinline__ bool wg_wait_geq(uint32_t* ctr, uint32_t target, Smem& s) {
+// Waits until *ctr >= target, then acquires. Returns false when a.wait_ticks
+// of the 100 MHz wall clock (s_memrealtime) pass first, or at once when
+// wait_ticks is 0 (a host-forced give-up), and then counts the timeout in
+// *a.timeouts. The counter is polled with relaxed loads (they read past this
+// XCD's L2 without invalidating it); the one acquire comes after the wait.
+__device__ __forceinline__ bool wg_wait_geq(const KernelArgs& a, uint32_t* ctr, uint32_t target,
+                                            Smem& s) {
   if (threadIdx.x == 0) {
-    uint32_t n = 0, ok = 1;
-    while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++n > kSpinLimit) {
-        ok = 0;
-        break;
+    uint32_t ok = 0;
+    const uint64_t limit = a.wait_ticks;
+    if (limit) {
+      const uint64_t t0 = wall_clock64();
+      for (;;) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) {
+          ok = 1;
+          break;
+        }
+        if (wall_clock64() - t0 > limit) break;
+        __builtin_amdgcn_s_sleep(1);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (!ok && a.timeouts) __hip_atomic_fetch_add(a.timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s.misc_u[3] = ok;
   }
   __syncthreads();
@@ -3866,7 +3882,7 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   LUMEN_TICK("p_pass1", b);
   if ((kDebugStop & 255u) == 2u) return;
   wg_arrive(&ws.bar, 0xffffffffu, s);
-  const bool ok = wg_wait_geq(&ws.bar, G, s);
+  const bool ok = wg_wait_geq(a, &ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("p_barrier", b);
@@ -4115,7 +4131,9 @@ __device__ __forceinline__ void block_row(const KernelArgs& a, uint32_t& b, uint
 // The workgroup that arrived last on its row's counter restores the row's
 // coordination block once it is done. Every other workgroup of the row has
 // arrived before it and no longer touches the block; the next launch sees
-// the cleared block (kernel boundary).
+// the cleared block (kernel boundary). One exception: a top-p finisher that
+// gave up waiting for its S1 walker leaves the reset to the walker
+// (res_s1_walker), whose release is then the block's last access.
 __device__ __forceinline__ void row_reset(const KernelArgs& a, uint32_t b, Smem& s) {
   __syncthreads();
   if (threadIdx.x == 0 && s.finisher) {

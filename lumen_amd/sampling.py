@@ -153,6 +153,19 @@ class Engine:
         except Exception:
             pass
 
+    def set_wait_limit(self, microseconds: int):
+        """Bound of every cross-workgroup wait (lumen_sampler_set_wait_limit);
+        0 makes every such wait give up at once."""
+        _native.check(_native.load().lumen_sampler_set_wait_limit(self._h, int(microseconds)),
+                      "lumen_sampler_set_wait_limit")
+
+    def wait_timeouts(self) -> int:
+        """Cross-workgroup waits that gave up since the context was created."""
+        n = ctypes.c_uint64()
+        _native.check(_native.load().lumen_sampler_wait_timeouts(self._h, ctypes.byref(n)),
+                      "lumen_sampler_wait_timeouts")
+        return int(n.value)
+
     def prepare(self, logits, params: Sequence[SamplingParams], **kw) -> "PreparedBatch":
         """A reusable batch description (see PreparedBatch)."""
         return PreparedBatch(self, logits, params, **kw)
