@@ -240,9 +240,13 @@ int lumen_sampler_sample_batch(lumen_sampler *s, const lumen_batch *batch, lumen
  * the library itself, so a call takes at most 8 rows of at most 262144
  * logits, no device history (hist_ring_dev), at most 65536 form-A penalty
  * entries, and anti_restate rows need guard_out; anything beyond returns
- * LUMEN_ERR_INVALID with lumen_sampler_last_error() naming the limit. Every
- * call on a GPU shares that GPU's array (from every context and thread):
- * calls that overlap on one GPU race, so serialize them (one stream). */
+ * LUMEN_ERR_INVALID with lumen_sampler_last_error() naming the limit. The
+ * array of a GPU belongs to the first context that makes a no-allocation
+ * call there, until that context is destroyed; calls from other contexts
+ * return LUMEN_ERR_INVALID. Calls of the owning context share the array, so
+ * they must not overlap: issue them on one stream (the convention for every
+ * context). Under stream capture, form-A histories are refused (their counts
+ * would be copied from host memory at every replay): pass pen_offsets. */
 int lumen_sampler_sample_batch_noalloc(lumen_sampler *s, const lumen_batch *batch,
                                        lumen_stream stream);
 

@@ -35,9 +35,6 @@
 
 namespace lumen {
 
-#ifdef LUMEN_EST_STOP
-__device__ int g_est_stop;
-#endif
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
@@ -440,15 +437,9 @@ __device__ __forceinline__ bool est_prepare(const float (&x)[M], double p_start,
     nb += sh.red_b[i];
   }
   et.run = before_w + __popcll(bm & ((1ull << lane) - 1ull));
-#ifdef LUMEN_TICK_FINAL
-  LUMEN_TICK("p1cn", 0);
-#endif
   SegVal v{et.boundary, et.own};
   SegVal prev;
   SegVal inc = seg_scan_incl(v, sh, es, &prev);
-#ifdef LUMEN_TICK_FINAL
-  LUMEN_TICK("p2sc", 0);
-#endif
 
   et.excl = (t == 0) ? PMap{0u, 0u} : prev.m;
   const bool fits = nb <= kEstMaxB && nb * M <= kEstBx;
@@ -512,15 +503,6 @@ __device__ __forceinline__ bool est_resolve(float c_in, const float (&x)[M], int
     float c = c_in;
     int fail = 0, hit_seg = -1, hit_pos = -1;
     float before = 0.f, cseg = 0.f;
-#ifdef LUMEN_TICK_FINAL
-    {
-      float acc = 0.f;
-#pragma unroll
-      for (int q = 0; q < M; ++q) acc += bx_r[q];
-      if (acc == 1234.5f && sb_r == 7u && a0_r == 3u && a1_r == 5u && bp_r == 9u) es.fail = 7;
-      LUMEN_TICK("r0pf", 0);
-    }
-#endif
     if (regs) {
       // Branch-free walk. The only dependent chain per boundary is the
       // parity-selected run increment and the M sequential adds; the checks
@@ -612,9 +594,6 @@ __device__ __forceinline__ bool est_resolve(float c_in, const float (&x)[M], int
       }
     }
     if (lane == 0) {
-#ifdef LUMEN_TICK_FINAL
-      LUMEN_TICK("r1wk", 0);
-#endif
       es.fail = fail;
       es.hit_seg = hit_seg;
       es.hit_pos = hit_pos;
@@ -686,10 +665,6 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
                                                       float theta, EcssShared& sh, EstShared& es,
                                                       double* wsum, int nact = kThreads) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-#ifdef LUMEN_TICK_FINAL
-  __syncthreads();
-  LUMEN_TICK("e_x", 0);
-#endif
   double d = 0.0;
 #pragma unroll
   for (int j = 0; j < M; ++j) d += (double)x[j];
@@ -703,28 +678,13 @@ __device__ __forceinline__ EcssResult ecss_fast_chunk(float c, const float (&x)[
   __syncthreads();
   const double p_start = (double)c + pre + inc - d;
   const double rel = (double)((t + 1) * M) * 0x1.0p-24 * 1.01 + 1e-9;
-#ifdef LUMEN_EST_STOP
-  if (g_est_stop == 1) { EcssResult z{c, 0, -1, 0.f}; return z; }
-#endif
-#ifdef LUMEN_TICK_FINAL
-  LUMEN_TICK("e_scan", 0);
-#endif
   EstThread et;
   EcssResult r;
   if (!est_prepare<M>(x, p_start, d, rel, sh, es, et, nact)) {
     if (t == 0) es.fail = 2;  // structure did not fit (diagnostic only)
     return ecss_chunk<M>(c, x, mode, theta, sh);
   }
-#ifdef LUMEN_EST_STOP
-  if (g_est_stop == 2) { EcssResult z{c, 0, -1, 0.f}; return z; }
-#endif
-#ifdef LUMEN_TICK_FINAL
-  LUMEN_TICK("e_prep", 0);
-#endif
   if (est_resolve<M>(c, x, mode, theta, et, sh, es, &r)) {
-#ifdef LUMEN_TICK_FINAL
-    LUMEN_TICK("e_resolved", 0);
-#endif
     return r;
   }
   return ecss_chunk<M>(c, x, mode, theta, sh);
@@ -762,9 +722,6 @@ __device__ __forceinline__ EcssResult ecss_chunk4(float c, const float (&x)[4], 
   }
   __syncthreads();
   const double P = (double)c + dp[w] + (winc - d);
-#ifdef LUMEN_EST_STOP
-  if (g_est_stop == 11) { EcssResult z{c, 0, -1, 0.f}; return z; }
-#endif
 
   const double rel = (double)(4 * t + 4) * 0x1.0p-24 * 1.001 + 1e-12;
   const uint32_t lo = est_binade(P * (1.0 - rel));
@@ -810,9 +767,6 @@ __device__ __forceinline__ EcssResult ecss_chunk4(float c, const float (&x)[4], 
   const SegVal ex = seg_combine(SegVal{es.pxh[w], es.pxm[w]}, wave_shr1(inc, id));
   const uint32_t bidx = es.pxc[w] + (uint32_t)__popcll(bm & ((1ull << lane) - 1ull));
   const int nb = es.nb;
-#ifdef LUMEN_EST_STOP
-  if (g_est_stop == 12) { EcssResult z{c, 0, -1, 0.f}; return z; }
-#endif
 
   if (nb > 63) {
     __syncthreads();
@@ -835,9 +789,6 @@ __device__ __forceinline__ EcssResult ecss_chunk4(float c, const float (&x)[4], 
     es.seg_tot[nb] = bnd ? PMap{0u, 0u} : seg_combine(ex, SegVal{0u, m}).m;
   }
   __syncthreads();
-#ifdef LUMEN_EST_STOP
-  if (g_est_stop == 13) { EcssResult z{c, 0, -1, 0.f}; return z; }
-#endif
 
   // 3. the walk over runs and boundaries, on wave 0 (uniform values)
   if (w == 0) {

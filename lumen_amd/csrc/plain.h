@@ -219,28 +219,6 @@ __device__ __forceinline__ void temp_res(const KernelArgs& a, int b, uint32_t sl
     good = s.misc_u[0] != 0u && s.misc_u[1] != 0u;
   }
   if (!good) {
-#ifdef LUMEN_FALLBACK_DEBUG
-    // development builds: the token tells why (no fallback)
-    if (t == 0 && s.misc_u[0] == 0u && nit > 0u) {
-      // the walk failed: reason (1 map outside its binade, 2 crossing in a
-      // run), the item, and whether the item's binade is above or below
-      const uint32_t* items = reinterpret_cast<const uint32_t*>(s.Bk);
-      const uint32_t bin = items[4u * s.misc_u[2]];
-      const uint32_t cbx = __float_as_uint(s.red_f[1]);
-      a.tokens[b] = 0xe0000000u | (s.misc_u[3] << 24) | ((cbx & 0xff800000u) > bin ? 0x800000u : 0u) |
-                    (min(s.misc_u[2], 0xfffu) << 8) | min(nit, 255u);
-    } else if (t == 0) {
-      uint32_t anyf = 0, nr = 0, ni = 0;
-      for (uint32_t i = 0; i < Gv; ++i) {
-        anyf |= ws.part_nrec[i] == 0xffffffffu ? 1u : 0u;
-        nr += ws.part_nraw[i];
-        ni += ws.part_nrec[i] == 0xffffffffu ? 0u : ws.part_nrec[i];
-      }
-      a.tokens[b] = 0xf0000000u | (anyf << 27) | (__hip_atomic_load(&ws.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 24) |
-                    (min(nr, 4095u) << 12) | min(ni, 4095u);
-    }
-    return;
-#endif
     row_single<false>(a, b, s);
     return;
   }

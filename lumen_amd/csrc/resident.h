@@ -45,20 +45,6 @@ constexpr uint32_t kNoRaw = 0xffffffffu;
 constexpr uint32_t kResWindowCap = (uint32_t)kCap / 2u;          // sorted in place with its own spare half
 static_assert((uint32_t)kMaxSlices * 32u <= (uint32_t)kRowRecs, "slice record areas fit the row");
 
-// Development aid: -DLUMEN_RES_STOP=k makes the rows of this path stop after
-// phase k (wrong tokens), so that the kernel time of each prefix of the
-// critical path can be measured. Never defined in the shipped build.
-#ifdef LUMEN_RES_STOP
-#define RES_STOP(k)                             \
-  do {                                          \
-    if (LUMEN_RES_STOP == (k)) {                \
-      if (threadIdx.x == 0) a.tokens[b] = 0u;   \
-      return;                                   \
-    }                                           \
-  } while (0)
-#else
-#define RES_STOP(k) do { } while (0)
-#endif
 
 __device__ __forceinline__ float* res_buf(Smem& s) { return reinterpret_cast<float*>(s.A); }
 
@@ -248,9 +234,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   __syncthreads();
   const double P = p_slice + pre + (dinc - d);
   const double floor_t = (double)fmaxf(fmaxf(lb, mpre), wave_shr1(minc, 0.f));
-#ifdef LUMEN_TIMING
   LUMEN_TICK("rr_scan", LUMEN_TIMING_ROW);
-#endif
   // the probe's margin is the drift of a probability sum from its estimate
   // (the exact softmax sum divided out, from the slice's exact start):
   // observed up to ~3e-5 of it; a sum estimated from the row start drifts
@@ -295,9 +279,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   // without an uncertain thread between them) and ends before anything else
   const bool head = act && (unc || prv != code);
   const bool last = act && !unc && nxt != code;
-#ifdef LUMEN_TIMING
   LUMEN_TICK("rr_maps", LUMEN_TIMING_ROW);
-#endif
   SegVal prev;
   const SegVal inc = seg_scan_incl(SegVal{head ? 1u : 0u, (act && !unc) ? own : PMap{0u, 0u}},
                                    s.ecss, s.est, &prev);
@@ -305,9 +287,7 @@ __device__ __forceinline__ RecCount res_record(const float* et, double p_slice, 
   uint32_t ptot;
   const uint32_t pos = block_excl_scan_u32(packed, s, &ptot);
   RecCount rc{ptot & 0xffffu, ptot >> 16, true};
-#ifdef LUMEN_TIMING
   LUMEN_TICK("rr_scans", LUMEN_TIMING_ROW);
-#endif
   if (rc.items > kResItemCap || rc.raws > kResRawCap) {
     rc.ok = false;
     return rc;
@@ -485,20 +465,11 @@ __device__ __forceinline__ void res_walk_at(uint32_t G, uint32_t nit, uint32_t r
           // a run: the crossing cannot lie in it
           if (FIND && r < __uint_as_float(cb + inc)) {
             good = 0;
-#ifdef LUMEN_FALLBACK_DEBUG
-            hit_k = k0 + q;
-            hit_j = 2u;
-#endif
             break;
           }
           cb += inc;
         } else {
           good = 0;
-#ifdef LUMEN_FALLBACK_DEBUG
-          hit_k = k0 + q;
-          hit_j = 1u;
-          before = cb;
-#endif
           break;
         }
         continue;
@@ -560,25 +531,24 @@ __device__ __forceinline__ void res_walk_at(uint32_t G, uint32_t nit, uint32_t r
   }
 }
 
-// res_walk_at with the running sum kept as a uniform value and no branch per
-// run item: every lane loads its item of the current 64 (and the raw
-// summands of an uncertain thread) up front, so a run costs one parity
-// select, one add and its checks, and an uncertain thread that must be
-// replayed is replayed by all lanes at once, each on its own item's
-// summands from the same exact start, lane q's result being the one kept.
-// Same results and outputs as res_walk_at; failed checks accumulate into a
-// flag tested once per 64 items.
-template <bool FIND>
-__device__ __forceinline__ void res_walk_fast(uint32_t G, uint32_t nit, uint32_t rawbase, float r,
-                                              const uint32_t* words, Smem& s,
-                                              float* starts = nullptr) {
+// The S1 walk of res_walk_at (sum mode) arranged for latency: every lane
+// loads its item of the current 64 (and the raw summands of an uncertain
+// thread) up front, and the items are applied 8 at a time without a taken
+// branch: a run, or an uncertain thread whose map applies, is one parity
+// select and one add with its checks; only an uncertain thread that must be
+// replayed leaves the straight line, and is replayed by all lanes at once,
+// each on its own item's summands from the same exact start, lane q's
+// result being the one kept. Same results and outputs as res_walk_at<false>
+// without slice starts; failed checks accumulate into a flag tested once per
+// 64 items.
+__device__ __forceinline__ void res_walk_sum(uint32_t G, uint32_t nit, uint32_t rawbase,
+                                             const uint32_t* words, Smem& s) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t* ib = s.H0;
   const uint32_t* rb = s.H0 + 32;
   const uint4* items = reinterpret_cast<const uint4*>(words);
   const float* raws = reinterpret_cast<const float*>(words + rawbase);
-  uint32_t cb = 0u, bad = 0u, found = 0u, hit_k = 0u, hit_j = 0u, before = 0u;
-  uint32_t ns = 0;  // next slice whose start is still to be recorded
+  uint32_t cb = 0u, bad = 0u;
   for (uint32_t k0 = 0; k0 < nit; k0 += 64u) {
     const uint32_t k = k0 + lane;
     uint4 it = make_uint4(0u, 0u, 0u, kNoRaw);
@@ -603,77 +573,38 @@ __device__ __forceinline__ void res_walk_fast(uint32_t G, uint32_t nit, uint32_t
         xr[4 * m + 3] = f.w;
       }
     }
+    LUMEN_TICK("wk_loaded", LUMEN_TIMING_ROW);
     const uint32_t cnt = min(64u, nit - k0);
-    for (uint32_t q = 0; q < cnt; ++q) {
-      if (!FIND && starts) {
-        while (ns < G && ib[ns] <= k0 + q) {
-          if (lane == 0) starts[ns] = __uint_as_float(cb);
-          ++ns;
-        }
-      }
-      const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
-      const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
-      const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
-      const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
-      const uint32_t inc = (cb & 1u) ? a1 : a0;
-      // the map applies: the exact sum is inside its binade and stays there
-      // (and, searching, stays at or below r)
-      const bool fits = (cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u &&
-                        !(FIND && r < __uint_as_float(cb + inc));
-      if (ro == kNoRaw) {
-        // a run: the crossing cannot lie in it, so a map that does not
-        // apply is a failed check
-        bad |= fits ? 0u : 1u;
-        cb = fits ? cb + inc : cb;
-        continue;
-      }
-      if (fits) {
-        cb += inc;
-        continue;
-      }
-      // an uncertain thread replayed from the exact start
-      float c = __uint_as_float(cb), cbef = c;
-      uint32_t hj = kResK;
+    for (uint32_t q0 = 0; q0 < cnt; q0 += 8u) {
 #pragma unroll
-      for (int j = 0; j < (int)kResK; ++j) {
-        const float y = __fadd_rn(c, xr[j]);
-        if (FIND) {
-          const bool h = hj == kResK && r < y;
-          cbef = h ? c : cbef;
-          hj = h ? (uint32_t)j : hj;
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t q = q0 + u;
+        const bool valid = q < cnt;
+        const uint32_t bin = (uint32_t)__builtin_amdgcn_readlane((int)it.x, (int)q);
+        const uint32_t a0 = (uint32_t)__builtin_amdgcn_readlane((int)it.y, (int)q);
+        const uint32_t a1 = (uint32_t)__builtin_amdgcn_readlane((int)it.z, (int)q);
+        const uint32_t ro = (uint32_t)__builtin_amdgcn_readlane((int)roff, (int)q);
+        const uint32_t inc = (cb & 1u) ? a1 : a0;
+        // the map applies: the exact sum is inside its binade and stays there
+        const bool fits = (cb & 0xff800000u) == bin && inc < kSat && cb + inc < bin + 0x00800000u;
+        // a run cannot hold a binade change: a map that does not apply fails
+        bad |= (valid && ro == kNoRaw && !fits) ? 1u : 0u;
+        cb = (valid && fits) ? cb + inc : cb;
+        if (__builtin_expect(valid && ro != kNoRaw && !fits, 0)) {
+          // an uncertain thread replayed from the exact start
+          float c = __uint_as_float(cb);
+#pragma unroll
+          for (int j = 0; j < (int)kResK; ++j) c = __fadd_rn(c, xr[j]);
+          cb = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(c), (int)q);
         }
-        c = y;
       }
-      if (FIND) {
-        const uint32_t hq = (uint32_t)__builtin_amdgcn_readlane((int)hj, (int)q);
-        if (hq < kResK) {
-          // the hit sum: the add at hj from the sum before it
-          const float cb4 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cbef), (int)q));
-          found = 1u;
-          hit_k = k0 + q;
-          hit_j = hq;
-          before = __float_as_uint(cb4);
-          cb = __float_as_uint(__fadd_rn(cb4, raws[ro + hq]));
-          break;
-        }
-      }
-      cb = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(c), (int)q);
     }
-    if (bad || found) break;
-  }
-  if (!FIND && !bad && starts) {
-    while (ns < G) {
-      if (lane == 0) starts[ns] = __uint_as_float(cb);
-      ++ns;
-    }
+    LUMEN_TICK("wk_batch", LUMEN_TIMING_ROW);
+    if (bad) break;
   }
   if (lane == 0) {
     s.misc_u[0] = bad ? 0u : 1u;
-    s.misc_u[1] = found;
-    s.misc_u[2] = hit_k;
-    s.misc_u[3] = hit_j;
     s.red_f[0] = __uint_as_float(cb);
-    s.red_f[1] = __uint_as_float(before);
   }
 }
 
@@ -736,16 +667,11 @@ __device__ __forceinline__ void res_s1_walker(const KernelArgs& a, int b, uint32
               res_gather(a, b, Gv, s, &nit, &rawbase);
   LUMEN_TICK("w_gathered", b);
   if (good) {
-    if (threadIdx.x < 64u)
-      res_walk_fast<false>(Gv, nit, rawbase, 0.f, reinterpret_cast<const uint32_t*>(s.Bk), s);
+    if (threadIdx.x < 64u) res_walk_sum(Gv, nit, rawbase, reinterpret_cast<const uint32_t*>(s.Bk), s);
     __syncthreads();
     good = s.misc_u[0] != 0u;
   }
   LUMEN_TICK("w_walked", b);
-#ifdef LUMEN_TIMING
-  if (threadIdx.x == 0 && b == LUMEN_TIMING_ROW)
-    printf("walker row %d: items %u raws %u\n", b, nit, s.H0[32 + Gv]);
-#endif
   if (threadIdx.x == 0) {
     if (good)
       ws.unused0 = __float_as_uint(s.red_f[0]);
@@ -777,12 +703,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
   LUMEN_TICK("r_start", b);
 
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 10) {
-    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-    return;
-  }
-#endif
   // ---- phase A ----
   float smp[4];
   res_sample_issue(row, smp);
@@ -790,15 +710,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   res_issue<BF16>(row, slice_bounds(V, Gv, sl * q), v);
   const uint32_t tau = res_sample_select(smp, V, kResCandTarget, s);
   const float tv = tau ? key2f(tau) : kNegInf;
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 11) {
-    float acc = 0.f;
-    for (int q = 0; q < 8; ++q) acc += v[q][0] + v[q][1] + v[q][2] + v[q][3];
-    if (acc == 1234.5f && tv == 3.f) a.tokens[b] = 7u;
-    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-    return;
-  }
-#endif
   float x[kResK];
   uint32_t cmask = 0, coff = 0;
   for (uint32_t j = 0; j < q; ++j) {
@@ -807,15 +718,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     if (j > 0) res_issue<BF16>(row, sc, v);
     res_load<BF16>(a, b, P, row, sc, pen, v, x, s);
     LUMEN_TICK("r_loaded", b);
-#ifdef LUMEN_RES_STOP
-    if (LUMEN_RES_STOP == 12) {
-      float acc = 0.f;
-      for (int q = 0; q < (int)kResK; ++q) acc += x[q];
-      if (acc == 1234.5f) a.tokens[b] = 7u;
-      if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-      return;
-    }
-#endif
     if (a.pen_out) {
       float* po = a.pen_out + (uint64_t)b * V + sc.lo + t * kResK;
 #pragma unroll
@@ -845,22 +747,10 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     }
   }
   LUMEN_TICK("r_phaseA", b);
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 13) {
-    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-    return;
-  }
-#endif
   wg_arrive(&ws.bar, 0xffffffffu, s);
   const bool ok = wg_wait_geq(a, &ws.bar, G, s);
   if (!ok && t == 0) __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("r_barrier", b);
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 1) {
-    if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-    return;
-  }
-#endif
 
   // ---- phase B ----
   // the last chunk first: its logits are still in registers
@@ -944,12 +834,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
       *reinterpret_cast<float4*>(Lt + 4 * qq) = make_float4(e0, e1, e2, e3);
     }
     LUMEN_TICK("rb_exps", b);
-#ifdef LUMEN_RES_STOP
-    if (LUMEN_RES_STOP == 2) {
-      if (wg_arrive(&ws.arrive, G - 1u, s) == G - 1u && t == 0) a.tokens[b] = 0u;
-      return;
-    }
-#endif
     const uint32_t bsh = res_bin_shift(tau ? expf_glibc_nonpos(__fsub_rn(tv, m1)) : 0.f);
     __syncthreads();  // the histogram is cleared
     {
@@ -985,7 +869,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   }
   if (arr != G - 1u) return;
   LUMEN_TICK("r_finisher", b);
-  RES_STOP(3);
   const uint32_t Gr = G;
   G = Gv;  // from here on, slices are the virtual slices
 
@@ -1041,7 +924,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     __syncthreads();
   }
   LUMEN_TICK("r_gathered", b);
-  RES_STOP(4);
   const float S1_hi = s.red_f[2];
   // Window: the lowest mass bin (from the top) whose running mass reaches
   // top_p * S1 with a margin, plus one spare bin, bounds the window from
@@ -1086,7 +968,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     if ((wmask >> q) & 1u) s.Bk[wo++] = ((uint64_t)(~ej[q]) << 32) | (kPer * t + (uint32_t)q);
   __syncthreads();
   LUMEN_TICK("r_window", b);
-  RES_STOP(6);
   // a window over half of list B sorts through list A (the candidates are
   // then read again from the row's buffer)
   const bool cand_lds = nw <= kResWindowCap;
@@ -1097,7 +978,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
     sort_u64_asc(s.Bk, nw, wtmp, s, hint);
   }
   LUMEN_TICK("r_sorted", b);
-  RES_STOP(7);
   // S1 from the walker (always released, also on failure)
   const bool got = wg_wait_geq(a, &ws.bar, 2u * Gr, s);
   if (t == 0) {
@@ -1145,7 +1025,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   const EcssResult wk = list_ecss_block(
       nw, [&](uint32_t j) { return __uint_as_float(~(uint32_t)(s.Bk[j] >> 32)); }, kEcssFindGe, P.top_p, 0.f, s);
   LUMEN_TICK("r_crossing", b);
-  RES_STOP(8);
   // the crossing's p must exceed every p outside the window, so no token
   // outside it ties with (or precedes) the kept set
   if (!wk.found || !(__uint_as_float(~(uint32_t)(s.Bk[wk.pos] >> 32)) > p_x)) {
@@ -1196,10 +1075,6 @@ __device__ __forceinline__ void topp_res(const KernelArgs& a, int b, uint32_t sl
   tr.pad[0] = 0;
   tr.pad[1] = ncand | (nw << 16);
   LUMEN_TICK("r_kept", b);
-#ifdef LUMEN_TIMING
-  if (t == 0 && b == LUMEN_TIMING_ROW) printf("finisher row %d: ncand %u nw %u kept %u nk %u\n", b, ncand, nw, (uint32_t)wk.pos + 1u, nk);
-#endif
-  RES_STOP(9);
   // the nucleus holds the row maximum m1 (the largest p)
   const uint32_t tok = final_on_list(a, P, nk, rdraw, s, tr, m1, pre_exp);
   LUMEN_TICK("r_final", b);

@@ -77,19 +77,12 @@ uint32_t plan_blocks(const std::vector<RowParams>& rows, uint32_t V, uint32_t ca
   const uint32_t kX = 8;
   const uint32_t bin_cap = cap / kX;
   std::vector<uint32_t> G(B, 1), w(B, 0);
-  // slice weights of the greedy, top-k and top-p paths; LUMEN_SAMPLER_WEIGHTS=g,k,p
-  // overrides them (a tuning aid)
+  // slice weights of the greedy, top-k and top-p paths (timed on the mixed
+  // config-3 batch and the defaults batch: 2,3,8 best)
   struct Weights {
     uint32_t g = 2, k = 3, p = 8;
   };
-  static const Weights wt = [] {
-    Weights x;
-    if (const char* e = std::getenv("LUMEN_SAMPLER_WEIGHTS")) {
-      unsigned g = 0, k = 0, p = 0;
-      if (std::sscanf(e, "%u,%u,%u", &g, &k, &p) == 3 && g && k && p) x = Weights{g, k, p};
-    }
-    return x;
-  }();
+  constexpr Weights wt{};
   uint64_t wsum = 0;
   uint32_t fixed = 0;
   for (uint32_t b = 0; b < B; ++b) {
@@ -618,10 +611,34 @@ int lumen_sampler_wait_timeouts(lumen_sampler* s, uint64_t* count) {
   return LUMEN_OK;
 }
 
+namespace {
+// The no-allocation array of each GPU belongs to one context at a time: the
+// first context that makes a no-allocation call on the GPU, until it is
+// destroyed. Calls from any other context are refused, so two contexts
+// cannot overlap on the array; a context itself is used on one stream at a
+// time (the header's convention), which serializes its own calls.
+std::mutex g_na_mu;
+lumen_sampler* g_na_owner[64] = {};
+
+bool noalloc_claim(lumen_sampler* s) {
+  if (s->device < 0 || s->device >= 64) return false;
+  std::lock_guard<std::mutex> lk(g_na_mu);
+  if (!g_na_owner[s->device]) g_na_owner[s->device] = s;
+  return g_na_owner[s->device] == s;
+}
+
+void noalloc_release(lumen_sampler* s) {
+  if (s->device < 0 || s->device >= 64) return;
+  std::lock_guard<std::mutex> lk(g_na_mu);
+  if (g_na_owner[s->device] == s) g_na_owner[s->device] = nullptr;
+}
+}  // namespace
+
 void lumen_sampler_destroy(lumen_sampler* s) {
   if (!s) return;
   DeviceGuard g(s->device);
   (void)hipDeviceSynchronize();
+  noalloc_release(s);
   if (s->pin) (void)hipHostFree(s->pin);
   if (s->stage.p) (void)hipFree(s->stage.p);
   if (s->pen_scratch.p) (void)hipFree(s->pen_scratch.p);
@@ -641,6 +658,7 @@ void lumen_sampler_destroy(lumen_sampler* s) {
 namespace {
 int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, uint32_t* tok_map,
                  uint32_t* done_map, uint32_t* guard_map, bool sync, bool noalloc = false);
+
 }  // namespace
 
 int lumen_sampler_sample_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream) {
@@ -670,6 +688,10 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   if (!s || !bt) return fail(LUMEN_ERR_INVALID, "null context or batch");
   const uint32_t B = bt->batch, V = bt->vocab;
   if (noalloc) {
+    if (!noalloc_claim(s))
+      return fail(LUMEN_ERR_INVALID,
+                  "noalloc: this GPU's no-allocation array belongs to another context (one context "
+                  "per GPU may use it, until that context is destroyed)");
     if (B > lumen::kNoAllocMaxRows) return fail(LUMEN_ERR_INVALID, "noalloc: batch must be at most 8 rows");
     if (V > lumen::kNoAllocMaxVocab) return fail(LUMEN_ERR_INVALID, "noalloc: vocab must be at most 262144");
     if (bt->hist_ring_dev) return fail(LUMEN_ERR_INVALID, "noalloc: hist_ring_dev is not supported");
@@ -795,7 +817,7 @@ int launch_batch(lumen_sampler* s, const lumen_batch* bt, lumen_stream stream, u
   ka.slices = G;
   ka.xcd_rows = (B >= 8 && G > 1) ? 1u : 0u;
   uint32_t nblocks = G == 1 ? B : (ka.xcd_rows ? padded * G : B * G);
-  if (G > 1 && B >= 8 && !noalloc && std::getenv("LUMEN_SAMPLER_UNIFORM") == nullptr) {
+  if (G > 1 && B >= 8 && !noalloc) {
     const uint32_t nb = plan_blocks(rows, V, (uint32_t)s->max_resident, G, s->blk_map);
     if (nb) {
       nblocks = nb;

@@ -34,74 +34,18 @@
 #include "expf_glibc.h"
 #include "kernel_abi.h"
 
-// Development aid: -DLUMEN_DEBUG_STOP=k (only in development code objects)
-// makes the split top-p and top-k rows stop after phase k to price each
-// phase on the critical path. Release builds compile every check away.
-#ifdef LUMEN_DEBUG_STOP
-#define kDebugStop ((uint32_t)(LUMEN_DEBUG_STOP))
-#else
-#define kDebugStop 0u
-#endif
 
-// Development aid: -DLUMEN_TIMING records phase timestamps (100 MHz wall
-// clock) in thread 0 of the finishing workgroup of row 0 and prints them
-// once when that row's result is written.
+// Phase timestamps for development code objects (-DLUMEN_TIMING, devtrace.h);
+// in the shipped code object every tick compiles to nothing.
 #ifdef LUMEN_TIMING
-#include <cstdio>
-#ifndef LUMEN_TIMING_ROW
-#define LUMEN_TIMING_ROW 0
-#endif
-// one log per slice of the traced row in device memory; the workgroup's log
-// index (or -1) sits in LDS
-__device__ unsigned long long g_tick_t[16][64];
-__device__ const char* g_tick_l[16][64];
-__device__ int g_tick_n[16];
-__shared__ int g_tick_slot;
-__shared__ int g_nticks;
-#define LUMEN_TICK(label, b)                                                   \
-  do {                                                                        \
-    if (threadIdx.x == 0 && (b) == LUMEN_TIMING_ROW && g_tick_slot >= 0 && g_nticks < 64) {  \
-      g_tick_t[g_tick_slot][g_nticks] = wall_clock64();                       \
-      g_tick_l[g_tick_slot][g_nticks++] = label;                              \
-      g_tick_n[g_tick_slot] = g_nticks;                                       \
-    }                                                                         \
-  } while (0)
-#define LUMEN_TICK_INIT() \
-  do {                    \
-    if (threadIdx.x == 0) { g_nticks = 0; g_tick_slot = -1; } \
-  } while (0)
-#define LUMEN_TICK_SLOT(row, sl) \
-  do {                           \
-    if (threadIdx.x == 0) g_tick_slot = ((row) == LUMEN_TIMING_ROW && (sl) < 16) ? (int)(sl) : -1; \
-  } while (0)
-#define LUMEN_TICK_RESET(b) \
-  do {                      \
-    if (threadIdx.x == 0 && (b) == LUMEN_TIMING_ROW) g_nticks = 0; \
-  } while (0)
-// times from the earliest first tick of any slice of the row
-#define LUMEN_TICK_DUMP(b)                                                       \
-  do {                                                                          \
-    if (threadIdx.x == 0 && (b) == LUMEN_TIMING_ROW && g_tick_slot >= 0) {      \
-      unsigned long long t0_ = ~0ull;                                           \
-      for (int k_ = 0; k_ < 16; ++k_)                                           \
-        if (g_tick_n[k_] > 0 && g_tick_t[k_][0] < t0_) t0_ = g_tick_t[k_][0];   \
-      for (int k_ = 0; k_ < 16; ++k_)                                           \
-        if (k_ != g_tick_slot && g_tick_n[k_] > 0)                              \
-          for (int i_ = (g_tick_n[k_] > 3 ? g_tick_n[k_] - 3 : 0); i_ < g_tick_n[k_]; ++i_) \
-          printf("tick[%d] %s %f us\n", k_, g_tick_l[k_][i_], \
-                 (double)(g_tick_t[k_][i_] - t0_) / 100.0);       \
-      for (int i_ = 0; i_ < g_nticks; ++i_)                                     \
-        printf("tick[%d] %s %f us\n", g_tick_slot, g_tick_l[g_tick_slot][i_],  \
-               (double)(g_tick_t[g_tick_slot][i_] - t0_) / 100.0);              \
-      for (int k_ = 0; k_ < 16; ++k_) g_tick_n[k_] = 0;                         \
-    }                                                                           \
-  } while (0)
+#include "devtrace.h"
 #else
 #define LUMEN_TICK(label, b) do { } while (0)
 #define LUMEN_TICK_INIT() do { } while (0)
 #define LUMEN_TICK_SLOT(row, sl) do { } while (0)
 #define LUMEN_TICK_RESET(b) do { } while (0)
 #define LUMEN_TICK_DUMP(b) do { } while (0)
+#define LUMEN_ROW_TIMES(tr) do { } while (0)
 #endif
 
 #include "ecss.h"
@@ -979,6 +923,7 @@ __device__ __forceinline__ void write_result(const KernelArgs& a, int b, uint32_
     }
     a.tokens[b] = token;
     if (a.trace) {
+      LUMEN_ROW_TIMES(tr);
       tr.token = token;
       a.trace[b] = tr;
     }
@@ -1026,10 +971,6 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
     if (e.found) return (uint32_t)(s.A[e.pos] >> 32);
     return V - 1;
   }
-#ifdef LUMEN_TICK_FINAL
-  LUMEN_TICK_RESET(0);
-  LUMEN_TICK("final_start", 0);
-#endif
   // min-p (sampling.rs:976-994)
   bool mmask = false;
   float bound = 0.f;
@@ -1092,22 +1033,13 @@ __device__ __forceinline__ uint32_t final_on_list(const KernelArgs& a, const Row
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = expf_glibc(__fsub_rn(wv(j), m3));
   __syncthreads();
   LUMEN_TICK("fin_exps", LUMEN_TIMING_ROW);
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 20) return 0;
-#endif
   EcssResult S = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssSum, 0.f, 0.f, s);
   const float S3 = S.c;
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 21) return 0;
-#endif
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) xs[j] = __fdiv_rn(xs[j], S3);
   __syncthreads();
   LUMEN_TICK(s.est.fail == 2 ? "S3_nofit" : s.est.fail ? "S3_failed" : "S3_ok", LUMEN_TIMING_ROW);
   tr.final_sum = S3;
   EcssResult e = list_ecss_block(n, [&](uint32_t j) { return xs[j]; }, kEcssFindGt, r, 0.f, s);
-#ifdef LUMEN_RES_STOP
-  if (LUMEN_RES_STOP == 22) return 0;
-#endif
   LUMEN_TICK(s.est.fail == 2 ? "walk_nofit" : s.est.fail ? "walk_failed" : "walk_ok", LUMEN_TIMING_ROW);
   LUMEN_TICK("fin_walk", LUMEN_TIMING_ROW);
   tr.cdf_before = e.found ? e.before : e.c;
@@ -1188,15 +1120,6 @@ __device__ __forceinline__ EcssResult seq_ecss(const float* xs, uint32_t n, int 
   return r;
 }
 
-#ifdef LUMEN_WSP_STOP
-__device__ int g_wsp_stop;
-#define WSP_STOP(k)                    \
-  do {                                 \
-    if (g_wsp_stop == (k)) return true; \
-  } while (0)
-#else
-#define WSP_STOP(k) do { } while (0)
-#endif
 
 // f32::max folded in index order (NaN excluded by the caller): between equal
 // values (+0 and -0) the later one wins, as in fold(-inf, f32::max).
@@ -1260,7 +1183,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
   bool nan;
   const float m = small_max(v, act, nw, s, &nan);
   if (!is_finite(m) || nan) return false;
-  WSP_STOP(1);
   bool kept = act;
   float tp_sum = 0.f, tp_cum = 0.f;
   uint32_t tp_kept = 0;
@@ -1284,7 +1206,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
     if (act) pv[t] = p;
     if (wact && t >= n) pv[t] = 0.f;
     __syncthreads();
-    WSP_STOP(2);
     // rank of entry j in (p desc, idx asc) order: keys (~p << 32) | j (the
     // list is in idx order), four threads per entry, each over a quarter
     // of the list, 16 keys at a time
@@ -1317,7 +1238,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
     const uint32_t rk = act ? rank[t] : 0u;
     if (act) sp[rk] = p;
     __syncthreads();
-    WSP_STOP(3);
     if (t < 64u) {
       const EcssResult wr = seq_ecss(sp, n, kEcssFindGe, P.top_p);
       if (lane == 0) {
@@ -1331,7 +1251,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
     tp_cum = res[1];
     tp_kept = wpos >= 0 ? (uint32_t)wpos + 1u : V;
     if (wpos >= 0) kept = act && rk <= (uint32_t)wpos;
-    WSP_STOP(4);
   }
   // min-p (sampling.rs:976-994): the bound comes from the surviving
   // maximum, which top-p always keeps (it has the largest p)
@@ -1348,7 +1267,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
   // (inv_temp = inf) takes the general path below.
   const float m3 = (P.flags & kMinP) ? small_max(wv, kept, nw, s, &nan3) : __fmul_rn(m, P.inv_temp);
   if (!is_finite(m3) || nan3) return false;  // list and s.A untouched: the general path redoes it
-  WSP_STOP(5);
   float e3 = 0.f;
   if (wact) {
     e3 = kept ? expf_glibc(__fsub_rn(wv, m3)) : 0.f;
@@ -1361,7 +1279,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
   }
   __syncthreads();
   const float S3 = res[3];
-  WSP_STOP(6);
   if (act) xs[t] = kept ? __fdiv_rn(e3, S3) : 0.f;
   __syncthreads();
   if (t < 64u) {
@@ -1373,7 +1290,6 @@ __device__ __forceinline__ bool wave_small_path(const KernelArgs& a, int b, cons
     }
   }
   __syncthreads();
-  WSP_STOP(7);
   tr.path |= 2u;
   if (do_topp) {
     tr.topp_sum = tp_sum;
@@ -1487,10 +1403,6 @@ __device__ __forceinline__ void small_path(const KernelArgs& a, int b, const Row
     nlist = nk;
   }
   LUMEN_TICK("small_before_final", b);
-  if ((kDebugStop >> 8) == 6u && !(P.flags & kTopP && tr.path == 4u)) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   uint32_t tok = final_on_list(a, P, nlist, rdraw, s, tr, known_max);
   LUMEN_TICK("small_after_final", b);
   write_result(a, b, tok, tr);
@@ -3271,7 +3183,6 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   const bool pen = (P.flags & kPen) && hist_hi(a, b) > a.hist_off[b];
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, pen);
   LUMEN_TICK("topk_start", b);
-  if ((kDebugStop >> 8) == 15u) return;
   uint32_t tau;
   const uint32_t* bm;
   if (k <= (uint32_t)kThreads && sc_len_max(V, G) <= 16u * kThreads) {
@@ -3279,7 +3190,6 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
     tau = topk_collect16(row, sc, bm, k, s);
     LUMEN_TICK("topk_sampled", b);
-    if ((kDebugStop >> 8) == 1u) return;
   } else {
     // k up to 2048: 3k + 256 candidates; larger k use the whole row stride
     // of the candidate buffer, aiming at 2.5k + 256
@@ -3287,7 +3197,6 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
                                        : min(5u * k / 2u + 256u, (uint32_t)kTopKCandCap * 3u / 4u);
     tau = sample_threshold(row, V, target, s);
     LUMEN_TICK("topk_sampled", b);
-    if ((kDebugStop >> 8) == 1u) return;
     bm = pen ? slice_bitmap(a, b, sc, s) : nullptr;
     if (threadIdx.x == 0) s.cnt = 0;
     __syncthreads();
@@ -3315,7 +3224,6 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   }
   flush_candidates(cand, &ws.cand_n, s, kTopKCandCap);
   LUMEN_TICK("topk_compacted", b);
-  if ((kDebugStop >> 8) == 2u) return;
   const uint32_t old = wg_arrive(&ws.arrive, G - 1u, s);
   if (old != G - 1u) return;
   LUMEN_TICK("topk_finisher", b);
@@ -3332,10 +3240,6 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
   for (uint32_t j = threadIdx.x; j < n; j += kThreads) CL[j] = cand[j];
   __syncthreads();
   LUMEN_TICK("topk_loaded", b);
-  if ((kDebugStop >> 8) == 3u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   // candidate entries are (~key << 32) | idx
   auto ckey = [&](uint32_t j) { return ~(uint32_t)(CL[j] >> 32); };
   uint32_t cut, ns;
@@ -3380,18 +3284,10 @@ __device__ __forceinline__ void topk_split(const KernelArgs& a, int b, uint32_t 
     }
   }
   LUMEN_TICK("topk_sort1", b);
-  if ((kDebugStop >> 8) == 4u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   sort_u64_asc(s.A, ns, s.Bk, s);  // ascending index
   tr.topk_cutoff_key = cut;
   tr.topk_survivors = ns;
   LUMEN_TICK("topk_sorted", b);
-  if ((kDebugStop >> 8) == 5u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   small_path(a, b, P, ns, false, rdraw, s, tr);
   LUMEN_TICK("topk_done", b);
 }
@@ -3604,12 +3500,6 @@ __device__ __forceinline__ void chain_prepare(const KernelArgs& a, int b, uint32
     // only costs one wave's recomputation in the walk.
     const double rel = 4e-5 + 3e-9 * (double)(sc.lo + q * chunk);
     const uint32_t nthr = (sc.hi - (sc.lo + q * chunk) + (uint32_t)M - 1u) / (uint32_t)M;
-#ifdef LUMEN_DEBUG_RECORDS
-    if (b == 0 && (t & 63u) == 0 && w * 64u < nthr) {
-      const double pw = wave_read(pt, 0);
-      (void)pw;
-    }
-#endif
     if (w * 64u < nthr)
       wave_park<M>(x, pt, d, rel, min(64u, nthr - w * 64u),
                    rec_slot(a, b, (sl * (uint32_t)kChainMaxQ + q) * (uint32_t)kWaves + w));
@@ -3755,12 +3645,6 @@ __device__ __forceinline__ float chain_walk(const KernelArgs& a, int b, uint32_t
           if (wt < kSlotAbsent && rec_walk<M>(words + wt, y)) {
             c = y;
           } else {
-#ifdef LUMEN_DEBUG_RECORDS
-            if (lane == 0 && b == 0)
-              printf("walk: slot %u %s at c=%a (nb %u)\n", s0 + (uint32_t)tb,
-                     wt >= kSlotAbsent ? "missing" : "mismatch", c,
-                     wt < kSlotAbsent ? words[wt] : 0u);
-#endif
             stop = s0 + (uint32_t)tb;  // c is its exact start
             break;
           }
@@ -3842,10 +3726,8 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
   const Slice sc = slice_bounds(V, G, sl);
   if (a.pen_out) slice_pen_out(a, b, row, sc, P, false);
   LUMEN_TICK("p_start", b);
-  if ((kDebugStop & 255u) == 15u) return;
   const uint32_t tau = sample_threshold(row, V, 6000u, s);
   LUMEN_TICK("p_sampled", b);
-  if ((kDebugStop & 255u) == 1u) return;
   const float tv = tau ? key2f(tau) : kNegInf;
   const float lo_v = tau ? __fsub_rn(tv, __fmul_rn(fabsf(tv) + 64.f, 0x1p-10f)) : kNegInf;
   float mt = kNegInf;
@@ -3880,13 +3762,11 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     ws.part_e[sl] = es_tot;
   }
   LUMEN_TICK("p_pass1", b);
-  if ((kDebugStop & 255u) == 2u) return;
   wg_arrive(&ws.bar, 0xffffffffu, s);
   const bool ok = wg_wait_geq(a, &ws.bar, G, s);
   if (!ok && threadIdx.x == 0)
     __hip_atomic_fetch_or(&ws.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   LUMEN_TICK("p_barrier", b);
-  if ((kDebugStop & 255u) == 3u) return;
   float m1 = kNegInf;
   uint32_t anynan = 0;
   double p_slice = 0.0;
@@ -3908,7 +3788,6 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     else chain_prepare<32>(a, b, sl, row, sc, m1, p_slice, s);
   }
   LUMEN_TICK("p_prepared", b);
-  if ((kDebugStop & 255u) == 4u) return;
   if (wg_arrive(&ws.arrive, G - 1u, s) != G - 1u) {
     LUMEN_TICK("p_not_finisher", b);
     LUMEN_TICK_DUMP(b);
@@ -3955,18 +3834,10 @@ __device__ __forceinline__ void topp_split(const KernelArgs& a, int b, uint32_t 
     __syncthreads();
   }
   LUMEN_TICK("p_gathered", b);
-  if ((kDebugStop & 255u) == 5u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   uint32_t nre;
   const float S1 = m16 ? chain_walk<16>(a, b, G, row, m1, &nre, s)
                        : chain_walk<32>(a, b, G, row, m1, &nre, s);
   LUMEN_TICK("p_chain", b);
-  if ((kDebugStop & 255u) == 6u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   RowTrace tr;
   init_trace(tr, V);
   tr.path = 4u;
@@ -4040,10 +3911,6 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   const uint32_t n = s.cnt;
   LUMEN_TICK("p_window_built", b);
-  if ((kDebugStop & 255u) == 7u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   {
     // keys (~p bits << 32) | id with p in [p_lo, 1/S1]: their common high
     // bits are known without a reduction
@@ -4052,10 +3919,6 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
     sort_u64_asc(s.Bk, n, s.A, s, hint);
   }
   LUMEN_TICK("p_window_sorted", b);
-  if ((kDebugStop & 255u) == 8u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   // the sorted probabilities into a padded float array (list A is free
   // after the sort)
   float* ps = reinterpret_cast<float*>(s.A);
@@ -4064,10 +3927,6 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   EcssResult wk = list_ecss(n, [&](uint32_t j) { return ps[pad16(j)]; }, kEcssFindGe, P.top_p, 0.f, s);
   LUMEN_TICK(s.est.fail == 2 ? "p_walk_nofit" : s.est.fail ? "p_walk_failed" : "p_walk_ok", b);
-  if ((kDebugStop & 255u) == 9u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   if (!wk.found) {
     row_single<false>(a, b, s);
     return;
@@ -4083,10 +3942,6 @@ __device__ __forceinline__ void topp_window(const KernelArgs& a, int b, const Ro
   __syncthreads();
   sort_u64_asc(s.A, nk, s.Bk, s, ((uint64_t)span_mask(a.vocab) << 32) | 0xffffffffull);
   LUMEN_TICK("p_kept_sorted", b);
-  if ((kDebugStop & 255u) == 10u) {
-    if (threadIdx.x == 0) a.tokens[b] = 0u;
-    return;
-  }
   // the kept set holds the row maximum m1
   small_path(a, b, P, nk, true, rdraw, s, tr, m1);
 }
