@@ -315,6 +315,21 @@ def logit_variants(name, w, total_bytes):
     return out
 
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def logit_buffers_note(lgs):
+    """What the rotated buffers mean for where a launch reads its logits."""
+    total = int(sum(lg.nbytes for lg in lgs))
+    if total > MALL_BYTES:
+        why = ("cycled so that every launch reads its logits from HBM, not from the "
+               "256 MB Infinity Cache")
+    else:
+        why = (f"{len(lgs)} buffers of {lgs[0].nbytes / 1e6:.2f} MB fit the 256 MB Infinity "
+               "Cache: this figure is for cache-resident logits")
+    return {"count": len(lgs), "bytes": total, "cache_resident": total <= MALL_BYTES, "why": why}
+
+
 def to_device(w, lg):
     import torch
 
@@ -454,9 +469,7 @@ def measure(eng, name, steps, warmup, graph, rotate_bytes, cpu=True, cpu_budget=
         "launch": mode,
         "stream_launches": {"samples_per_s": round(B * steps / el_stream, 1),
                             "kernel_ms": round(kern_stream, 5)},
-        "logit_buffers": {"count": nbuf, "bytes": int(sum(lg.nbytes for lg in lgs)),
-                          "why": "cycled so that every launch reads its logits from HBM, "
-                                 "not from the 256 MB Infinity Cache"},
+        "logit_buffers": logit_buffers_note(lgs),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(f"{kernel}_{name}_pmc.txt"),
